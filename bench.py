@@ -1,0 +1,202 @@
+#!/usr/bin/env python3
+"""Benchmark of the quantized-matmul hot path on one MI355X.
+
+Metric: int4 GEMV HBM GB/s (config 2: W 14336 x 4096 int4 g32,
+fp16 scales, fp16 x -> fp16 y) plus int4 dequant-GEMM TFLOP/s at M = 2048
+(config 4).  A "step" is one call of the path over one batch; `value` is the
+GEMV's whole-job throughput in GB/s with every input resident in HBM.
+
+Timing: the K timed launches are captured once into a HIP graph (through torch's
+graph API on the plugin's stream) and replayed, bracketed by HIP events on that
+stream.  Weight/scale copies rotate over >= 512 MB so the 256 MB MALL cannot hold
+them.  The CPU baseline times the oracle (a C restatement of the reference WGSL,
+OpenMP) on the host cores.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+sys.path.insert(0, os.path.join(ROOT, "tests"))
+
+HBM_PEAK_GBS = 8000.0
+MFMA_F16_PEAK_TFLOPS = 2500.0
+
+C2 = dict(n_out=14336, k=4096, gs=32)
+C2_BYTES = 14336 * 4096 // 2 + 14336 * (4096 // 32) * 2 + 4096 * 2 + 14336 * 2  # 33,067,008
+C4 = dict(n_out=14336, k=4096, m=2048, gs=32)
+C4_FLOPS = 2 * 2048 * 14336 * 4096
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+def timed_graph(torch, ctx, launch, steps: int, warmup: int):
+    """Warm up eagerly, capture `steps` launches into one graph, replay it once
+    untimed and once timed.  Returns seconds for the timed replay."""
+    s = torch.cuda.Stream()
+    ctx.set_stream(s.cuda_stream)
+    ctx.set_synchronous(False)
+    for i in range(warmup):
+        launch(i)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        for i in range(steps):
+            launch(i)
+    with torch.cuda.stream(s):
+        g.replay()
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record(s)
+    with torch.cuda.stream(s):
+        g.replay()
+    e1.record(s)
+    e1.synchronize()
+    torch.cuda.synchronize()
+    ctx.set_stream(None)
+    ctx.set_synchronous(True)
+    return e0.elapsed_time(e1) / 1e3
+
+
+def bench_c2(torch, W, ctx, steps, warmup):
+    from util import int4_weights
+    r = np.random.default_rng(2)
+    _, Wp, s = int4_weights(r, C2["n_out"], C2["k"], C2["gs"])
+    x = r.standard_normal(C2["k"]).astype(np.float16)
+    copies = max(2, -(-512 * 2**20 // (Wp.nbytes + s.nbytes)))
+    wbs = [ctx.upload(Wp) for _ in range(copies)]
+    sbs = [ctx.upload(s) for _ in range(copies)]
+    xb = ctx.upload(x)
+    yb = ctx.alloc(C2["n_out"] * 2)
+    d = W.qdesc(C2["n_out"], C2["k"], 1, 4, C2["gs"], W.NIBBLE_OFFSET_BINARY, W.SCALE_F16,
+                W.F16, W.F16)
+
+    def launch(i):
+        ctx.qmatmul(d, wbs[i % copies], sbs[i % copies], xb, None, yb)
+
+    sec = timed_graph(torch, ctx, launch, steps, warmup)
+    per = sec / steps
+    return {"sec": sec, "per_launch_s": per, "gbs": C2_BYTES / per / 1e9, "copies": copies,
+            "W": Wp, "s": s, "x": x}
+
+
+def bench_c4(torch, W, ctx, steps, warmup):
+    from util import bf16_bits, int4_weights
+    r = np.random.default_rng(4)
+    _, Wp, s = int4_weights(r, C4["n_out"], C4["k"], C4["gs"])
+    X = bf16_bits(r.standard_normal((C4["m"], C4["k"])).astype(np.float32))
+    wb, sb, xb = ctx.upload(Wp), ctx.upload(s), ctx.upload(X)
+    yb = ctx.alloc(C4["m"] * C4["n_out"] * 2)
+    d = W.qdesc(C4["n_out"], C4["k"], C4["m"], 4, C4["gs"], W.NIBBLE_OFFSET_BINARY, W.SCALE_F16,
+                W.BF16, W.BF16)
+    ctx.qmatmul(d, wb, sb, xb, None, yb)  # raises NOT_SUPPORTED if no kernel
+
+    def launch(i):
+        ctx.qmatmul(d, wb, sb, xb, None, yb)
+
+    n = max(3, min(steps, 50))
+    sec = timed_graph(torch, ctx, launch, n, max(1, warmup // 4))
+    per = sec / n
+    tf = C4_FLOPS / per / 1e12
+    return {"per_launch_s": per, "tflops": tf, "frac": tf / MFMA_F16_PEAK_TFLOPS, "steps": n}
+
+
+def cpu_baseline_c2(Wp, s, x, budget_s=10.0):
+    import oracle
+    sf = s.astype(np.float32).reshape(-1)
+    xf = x.astype(np.float32).reshape(-1, 1)
+    oracle.matmul_nax_grouped(Wp, sf, xf, C2["gs"])  # warm
+    n, t0 = 0, time.perf_counter()
+    while True:
+        oracle.matmul_nax_grouped(Wp, sf, xf, C2["gs"])
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s or n >= 200:
+            break
+    return {"value": round(C2_BYTES * n / el / 1e9, 3), "unit": "GB/s",
+            "cores": oracle.num_threads(), "kind": "port",
+            "sample": f"full config-2 GEMV (14336x4096 int4 g32) x{n} calls in {el:.1f} s, "
+                      "oracle/lux_oracle.c lo_matmul_nax_grouped (WGSL restatement, OpenMP)"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-budget", type=float, default=10.0)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU only (--gpus {args.gpus} requested); "
+              "the path shards over output channels with no communication, see DESIGN.md",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    import webgpu_amd as W
+
+    plugin = W.Plugin()
+    ctx = plugin.create_context(0)
+    log(f"device: {ctx.info().name.decode()}")
+    log("bench: config 2 int4 GEMV")
+    c2 = bench_c2(torch, W, ctx, args.steps, args.warmup)
+    log(f"  C2 {c2['per_launch_s']*1e6:.2f} us/launch, {c2['gbs']:.1f} GB/s")
+    c4 = None
+    try:
+        log("bench: config 4 int4 GEMM M=2048")
+        c4 = bench_c4(torch, W, ctx, args.steps, args.warmup)
+        log(f"  C4 {c4['per_launch_s']*1e6:.1f} us/launch, {c4['tflops']:.1f} TFLOP/s")
+    except W.LuxError as e:
+        log(f"  C4 skipped: {e}")
+    cpu = None
+    if not args.no_cpu_baseline:
+        log("bench: CPU baseline (oracle)")
+        cpu = cpu_baseline_c2(c2["W"], c2["s"], c2["x"], args.cpu_budget)
+        log(f"  CPU {cpu['value']} GB/s on {cpu['cores']} threads")
+
+    gbs = c2["gbs"]
+    out = {
+        "metric": "int4 GEMV HBM GB/s (% of 8 TB/s) + int4 GEMM TFLOPS (% MFMA peak) @M=2048",
+        "value": round(gbs, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(c2["per_launch_s"] * 1e3, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int4 weights, fp16 activations/scales, fp32 accumulate",
+        "data": "synthetic (seeded numpy, BASELINE.json config 2 distributions)",
+        "config": {"workload": "config 2: int4 g32 weight-only GEMV, W 14336x4096 offset-binary, "
+                               "fp16 scales U(0.005,0.02), x fp16 N(0,1), y fp16",
+                   "n_out": 14336, "k": 4096, "m": 1, "group_size": 32,
+                   "weight_copies_rotated": c2["copies"], "timing": "hip graph of K launches"},
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None},
+        "cpu_baseline": cpu,
+        "int4_gemm_m2048": None if c4 is None else {
+            "value": round(c4["tflops"], 2), "unit": "TFLOP/s",
+            "us_per_launch": round(c4["per_launch_s"] * 1e6, 2),
+            "roofline": {"bound": "mfma", "achieved": round(c4["tflops"], 2),
+                         "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                         "frac": round(c4["frac"], 4), "traffic": None}},
+    }
+    print(json.dumps(out), flush=True)
+    ctx.close()
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,149 @@
+/*
+ * lux/gpu/hip_quant.h -- quantized-matmul entry points of libluxgpu_backend_hip.so.
+ *
+ * ABI v3 has exactly one matmul slot, op_matmul_f32 (reference
+ * src/webgpu_plugin.cpp:1721-1771, vtable :4046).  The GEMV and quantized kernels
+ * of the reference are library shaders with no vtable slot and no host bridge
+ * (gemv.wgsl, quantized_nax.wgsl, quantized.wgsl, fp_quantized.wgsl).  This
+ * header gives them one: extra extern "C" symbols that a loader resolves with
+ * dlsym next to lux_gpu_backend_init.  Each function below names the reference
+ * interface it replaces.
+ *
+ * Conventions shared by every entry point:
+ *   - handles are the plugin's own LuxBackendContext / LuxBackendBuffer;
+ *   - weights W are [n_out x k] row-major, packed along k (int4: 8 per u32, value i
+ *     of a word in bits 4i..4i+3; int8: one byte each), the flat index being
+ *     r*k + kk exactly as in the WGSL (quantized_nax.wgsl:587-593);
+ *   - activations X are [m x k] and outputs Y [m x n_out], token-major.  For m == 1
+ *     this is the reference layout; for m > 1 the reference's act[k*N + c] and
+ *     out[r*N + c] are X^T and Y^T;
+ *   - every call is synchronous by default (returns after the device finished,
+ *     like dispatchCompute at src/webgpu_plugin.cpp:1005-1051); see
+ *     lux_hip_context_set_synchronous.
+ */
+#ifndef LUX_GPU_HIP_QUANT_H
+#define LUX_GPU_HIP_QUANT_H
+
+#include "lux/gpu/backend_plugin.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define LUX_HIP_QUANT_API_VERSION 1u
+
+/* Element types.  The first four keep LuxDtype's numbering (docs/api.md:188-197). */
+typedef enum LuxHipDtype {
+    LUX_HIP_F32 = 0,
+    LUX_HIP_F16 = 1,
+    LUX_HIP_BF16 = 2,
+    LUX_HIP_I32 = 3,
+    LUX_HIP_I8 = 32, /* not in LuxDtype: int8 activations (W4A8) */
+    LUX_HIP_I4 = 33  /* not in LuxDtype: packed int4 weights     */
+} LuxHipDtype;
+
+/* 4-bit value coding.  Offset-binary stores q+8 (quantized_nax.wgsl:94-112);
+ * two's complement stores q & 0xF (quantized.wgsl:124-156).  ob = tc ^ 0x8. */
+typedef enum LuxHipNibbleCoding {
+    LUX_HIP_NIBBLE_OFFSET_BINARY = 0,
+    LUX_HIP_NIBBLE_TWOS_COMPLEMENT = 1
+} LuxHipNibbleCoding;
+
+/* Per-group scale storage, [n_out x (k / group_size)] row-major. */
+typedef enum LuxHipScaleFormat {
+    LUX_HIP_SCALE_NONE = 0,       /* no scales: raw integer sums (W4A8, i32 out)   */
+    LUX_HIP_SCALE_F16 = 1,        /* IEEE binary16                                 */
+    LUX_HIP_SCALE_F32 = 2,        /* binary32                                      */
+    LUX_HIP_SCALE_GROUPSCALE = 3  /* 16-byte GroupScale {f32 scale, i32 zero_point,
+                                     f32 group_min, f32 group_max}
+                                     (quantized_nax.wgsl:49-54); only .scale used */
+} LuxHipScaleFormat;
+
+/* Descriptor of one weight-only (or W4A8) quantized matmul
+ *   Y[m, n] = sx[m] * sum_k (q(n, k) * s(n, k / group_size)) * X[m, k]
+ * sx is 1 unless X is int8 with per-token scales. */
+typedef struct LuxHipQMatmulDesc {
+    uint32_t struct_size;   /* sizeof(LuxHipQMatmulDesc)                          */
+    int32_t n_out;          /* weight rows = output channels                      */
+    int32_t k;              /* reduction length; k % 32 == 0                        */
+    int32_t m;              /* tokens (rows of X); 1 = GEMV                        */
+    int32_t weight_bits;    /* 4 or 8                                              */
+    int32_t group_size;     /* k elements per scale along k; k for per-row scales */
+    int32_t nibble_coding;  /* LuxHipNibbleCoding (4-bit weights only)            */
+    int32_t scale_format;   /* LuxHipScaleFormat                                   */
+    int32_t x_dtype;        /* F16, BF16, F32, or I8 (W4A8)                        */
+    int32_t y_dtype;        /* F16, BF16, F32, or I32 (W4A8 integer sums)          */
+    int32_t flags;          /* LUX_HIP_QFLAG_*                                     */
+} LuxHipQMatmulDesc;
+
+/* W4A8 with y_dtype I32 and group_size < k: write the per-group int32 partial
+ * sums P[m][n][g] instead of the full-k sum (checking aid, bit-exact). */
+#define LUX_HIP_QFLAG_GROUP_PARTIALS (1 << 0)
+
+/* Quantized matmul / GEMV.  Replaces, by descriptor:
+ *   matmul_nax_grouped  quantized_nax.wgsl:568-626  (weight_bits 4, offset-binary,
+ *                       group scales, fp activations; m == 1 is the GEMV case)
+ *   dequantize_nax_int8_group + matmul  quantized_nax.wgsl:364-386 +
+ *                       src/webgpu_plugin.cpp:138-205  (weight_bits 8)
+ *   matmul_int4_int8    quantized.wgsl:590-647  (weight_bits 4, two's complement,
+ *                       x_dtype I8, y_dtype I32, SCALE_NONE)
+ * x_scales is read only for x_dtype I8 with y_dtype != I32 (f32 [m]); pass NULL
+ * otherwise.  Returns INVALID_ARGUMENT for NULL handles, buffers smaller than the
+ * descriptor implies or inconsistent sizes, NOT_SUPPORTED for combinations without
+ * a kernel (the core then falls back to the CPU), DEVICE_LOST when the wait
+ * deadline (LUX_HIP_WAIT_TIMEOUT_S, default 5 s) expires. */
+LuxBackendError lux_hip_qmatmul(LuxBackendContext* ctx, const LuxHipQMatmulDesc* desc,
+                                LuxBackendBuffer* w, LuxBackendBuffer* w_scales,
+                                LuxBackendBuffer* x, LuxBackendBuffer* x_scales,
+                                LuxBackendBuffer* y);
+
+/* GemvParams of gemv.wgsl:21-30. */
+typedef struct LuxHipGemvParams {
+    uint32_t M;     /* rows of A                               */
+    uint32_t N;     /* columns of A                            */
+    float alpha;
+    float beta;     /* y is read only when beta != 0           */
+    uint32_t lda;   /* leading dimension of A (>= N)           */
+    uint32_t trans; /* 0: y[M] = alpha*A x + beta*y; 1: y[N] = alpha*A^T x + beta*y */
+    uint32_t _pad0;
+    uint32_t _pad1;
+} LuxHipGemvParams;
+
+/* fp32 GEMV, replaces gemv_row_parallel / gemv_vec4 / gemv_tiled / gemv_simple
+ * (trans 0, gemv.wgsl:49-96,155-274,360-381) and gemv_transpose (trans 1,
+ * gemv.wgsl:103-149); bindings 0..3 of the WGSL become a, x, y, params. */
+LuxBackendError lux_hip_gemv_f32(LuxBackendContext* ctx, LuxBackendBuffer* a,
+                                 LuxBackendBuffer* x, LuxBackendBuffer* y,
+                                 const LuxHipGemvParams* params);
+
+/* fp16 GEMV with fp32 accumulation: y[M] (f32) = A[M x N] (f16) . x[N] (f16).
+ * Replaces dot_product_fp16_fp32 (fp_quantized.wgsl:418-469) used with one shared
+ * vector.  lda in elements, even. */
+LuxBackendError lux_hip_gemv_f16(LuxBackendContext* ctx, LuxBackendBuffer* a,
+                                 LuxBackendBuffer* x, LuxBackendBuffer* y, uint32_t M,
+                                 uint32_t N, uint32_t lda);
+
+/* ---- buffer / stream plumbing (no reference counterpart: the WebGPU plugin
+ * hides device addresses, src/webgpu_plugin.cpp:1564) ------------------------ */
+
+/* Wrap caller-owned device memory as a buffer handle; buffer_free releases only
+ * the handle. */
+LuxBackendBuffer* lux_hip_buffer_wrap(LuxBackendContext* ctx, void* device_ptr, size_t bytes);
+void* lux_hip_buffer_device_ptr(LuxBackendBuffer* buf);
+size_t lux_hip_buffer_size(LuxBackendBuffer* buf);
+
+/* Run subsequent ops on `stream` (a hipStream_t; NULL restores the context's own). */
+LuxBackendError lux_hip_context_set_stream(LuxBackendContext* ctx, void* stream);
+void* lux_hip_context_get_stream(LuxBackendContext* ctx);
+/* synchronous != 0 (default): every op waits for completion before returning.
+ * 0: ops only enqueue; call vtbl->sync to wait. */
+LuxBackendError lux_hip_context_set_synchronous(LuxBackendContext* ctx, int synchronous);
+
+/* Message of the last failure on the calling thread ("" if none). */
+const char* lux_hip_last_error(void);
+uint32_t lux_hip_quant_api_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* LUX_GPU_HIP_QUANT_H */

@@ -1,0 +1,130 @@
+// Shared device helpers and kernel-launch declarations of libluxgpu_backend_hip.so.
+// Every kernel targets gfx950 (CDNA4): wave64, MFMA, 160 KB LDS per CU.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace luxhip {
+
+typedef _Float16 f16;
+typedef __attribute__((ext_vector_type(2))) _Float16 f16x2;
+typedef __attribute__((ext_vector_type(4))) _Float16 f16x4;
+typedef __attribute__((ext_vector_type(8))) _Float16 f16x8;
+typedef __attribute__((ext_vector_type(4))) float f32x4;
+typedef __attribute__((ext_vector_type(16))) float f32x16;
+typedef __attribute__((ext_vector_type(4))) int i32x4;
+typedef __attribute__((ext_vector_type(4))) unsigned int u32x4;
+typedef __attribute__((ext_vector_type(2))) unsigned int u32x2;
+typedef __attribute__((ext_vector_type(16))) int i32x16;
+
+// 16-byte GroupScale of quantized_nax.wgsl:49-54; kernels read .scale only.
+struct GroupScale {
+    float scale;
+    int32_t zero_point;
+    float group_min;
+    float group_max;
+};
+
+enum class ScaleKind : int { None = 0, F16 = 1, F32 = 2, GroupScale = 3 };
+enum class XKind : int { F32 = 0, F16 = 1, BF16 = 2, I8 = 32 };
+enum class YKind : int { F32 = 0, F16 = 1, BF16 = 2, I32 = 3 };
+
+#if defined(__HIP_DEVICE_COMPILE__) || defined(__HIPCC__)
+__device__ __forceinline__ float load_scale(const void* s, size_t idx, ScaleKind kind) {
+    switch (kind) {
+        case ScaleKind::F16: return (float)reinterpret_cast<const f16*>(s)[idx];
+        case ScaleKind::F32: return reinterpret_cast<const float*>(s)[idx];
+        case ScaleKind::GroupScale: return reinterpret_cast<const GroupScale*>(s)[idx].scale;
+        default: return 1.0f;
+    }
+}
+
+template <ScaleKind K>
+__device__ __forceinline__ float load_scale_t(const void* s, size_t idx) {
+    if constexpr (K == ScaleKind::F16) return (float)reinterpret_cast<const f16*>(s)[idx];
+    else if constexpr (K == ScaleKind::F32) return reinterpret_cast<const float*>(s)[idx];
+    else if constexpr (K == ScaleKind::GroupScale)
+        return reinterpret_cast<const GroupScale*>(s)[idx].scale;
+    else return 1.0f;
+}
+
+__device__ __forceinline__ float bf16_bits_to_f32(uint32_t b) {
+    return __builtin_bit_cast(float, b << 16);
+}
+
+// bfloat16 round-to-nearest-even (NaN kept quiet).
+__device__ __forceinline__ uint16_t f32_to_bf16_bits(float v) {
+    uint32_t x = __builtin_bit_cast(uint32_t, v);
+    if ((x & 0x7FFFFFFFu) > 0x7F800000u) return (uint16_t)((x >> 16) | 0x40u);
+    x += 0x7FFFu + ((x >> 16) & 1u);
+    return (uint16_t)(x >> 16);
+}
+
+template <YKind Y>
+__device__ __forceinline__ void store_y(void* y, size_t idx, float v) {
+    if constexpr (Y == YKind::F32) reinterpret_cast<float*>(y)[idx] = v;
+    else if constexpr (Y == YKind::F16) reinterpret_cast<f16*>(y)[idx] = (f16)v;  // RNE
+    else if constexpr (Y == YKind::BF16) reinterpret_cast<uint16_t*>(y)[idx] = f32_to_bf16_bits(v);
+    else reinterpret_cast<int32_t*>(y)[idx] = (int32_t)v;
+}
+
+template <XKind X>
+__device__ __forceinline__ float load_x(const void* x, size_t idx) {
+    if constexpr (X == XKind::F32) return reinterpret_cast<const float*>(x)[idx];
+    else if constexpr (X == XKind::F16) return (float)reinterpret_cast<const f16*>(x)[idx];
+    else if constexpr (X == XKind::BF16)
+        return bf16_bits_to_f32(reinterpret_cast<const uint16_t*>(x)[idx]);
+    else return (float)reinterpret_cast<const int8_t*>(x)[idx];
+}
+
+// Butterfly sum across the 64 lanes of a wave (every lane gets the total).
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+#endif
+
+// ---------------------------------------------------------------------------
+// Launchers (host side).  Plain pointers and sizes; shapes are validated by the
+// caller in plugin.hip before any launch, so every grid below stays in bounds.
+// ---------------------------------------------------------------------------
+struct QArgs {
+    const void* w;        // packed weights
+    const void* s;        // weight scales (may be null for ScaleKind::None)
+    const void* x;        // activations [m x k]
+    const float* xs;      // per-token activation scales [m] (W4A8) or null
+    void* y;              // output [m x n_out]
+    int n_out, k, m;
+    int group_size;
+    int wbits;            // 4 or 8
+    uint32_t xor_mask;    // 0x88888888 turns two's-complement nibbles into offset-binary
+    ScaleKind scale_kind;
+    XKind x_kind;
+    YKind y_kind;
+    bool group_partials;  // W4A8: write P[m][n][g]
+};
+
+hipError_t launch_gemv_f32(const float* A, const float* x, float* y, int M, int K, int lda,
+                           float alpha, float beta, hipStream_t s);
+hipError_t launch_gemv_f32_t(const float* A, const float* x, float* y, int M, int N, int lda,
+                             float alpha, float beta, hipStream_t s);
+hipError_t launch_gemm_f32(const float* A, const float* B, float* C, int M, int K, int N,
+                           hipStream_t s);
+hipError_t launch_gemv_f16(const void* A, const void* x, float* y, int M, int K, int lda,
+                           hipStream_t s);
+// int4 weight-only GEMV, m == 1.
+hipError_t launch_qgemv_i4(const QArgs& a, hipStream_t s);
+// Weight-only int4/int8 matmul for small m (bandwidth regime), fp16/bf16/f32 X.
+bool qgemm_small_supported(const QArgs& a);
+hipError_t launch_qgemm_small(const QArgs& a, hipStream_t s);
+// int4 grouped GEMM for large m (MFMA regime).
+bool qgemm_i4_large_supported(const QArgs& a);
+hipError_t launch_qgemm_i4_large(const QArgs& a, hipStream_t s);
+// W4A8 integer MFMA.
+bool w4a8_supported(const QArgs& a);
+hipError_t launch_w4a8(const QArgs& a, hipStream_t s);
+
+}  // namespace luxhip

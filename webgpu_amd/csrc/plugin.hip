@@ -1,0 +1,506 @@
+// libluxgpu_backend_hip.so -- Lux GPU backend plugin for AMD Instinct MI355X.
+//
+// Host side: plugin entry (lux_gpu_backend_init), the ABI-v3 vtable, device /
+// stream / buffer layer on HIP, and the quantized-matmul entry points of
+// <lux/gpu/hip_quant.h>.  Kernels live in the other .hip files of this directory.
+//
+// Reference counterparts (luxcpp/webgpu):
+//   plugin entry + vtable      src/webgpu_plugin.cpp:4018-4154
+//   context / device info      src/webgpu_plugin.cpp:1218-1430
+//   buffers                    src/webgpu_plugin.cpp:1432-1566
+//   bounded waits              src/webgpu_plugin.cpp:61-83 (timeout -> DEVICE_LOST)
+//   op_matmul_f32              src/webgpu_plugin.cpp:1721-1771
+// Differences by design: a context owns a hipStream_t instead of a queue and a
+// shared uniform buffer; kernel arguments travel with each launch, so ops on
+// different contexts (or threads) never share parameter memory.
+#include <algorithm>
+#include <chrono>
+#include <cstdarg>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <string>
+#include <thread>
+
+#include "common.hpp"
+#include "lux/gpu/backend_plugin.h"
+#include "lux/gpu/hip_quant.h"
+
+#define LUX_EXPORT extern "C" __attribute__((visibility("default")))
+
+namespace {
+
+using namespace luxhip;
+
+thread_local std::string g_last_error;
+
+LuxBackendError fail(LuxBackendError code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+LuxBackendError fail(LuxBackendError code, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_last_error = buf;
+    return code;
+}
+
+struct HipCtx {
+    int device = 0;
+    hipStream_t own_stream = nullptr;
+    hipStream_t stream = nullptr;
+    bool synchronous = true;
+    double timeout_s = 5.0;
+    std::string name;
+    std::string force_fail;  // LUX_HIP_FORCE_FAIL test hook: op name that fails
+    hipDeviceProp_t props{};
+};
+
+struct HipBuf {
+    void* ptr = nullptr;
+    size_t size = 0;
+    bool owned = true;
+    int device = 0;
+};
+
+inline HipCtx* C(LuxBackendContext* c) { return reinterpret_cast<HipCtx*>(c); }
+inline HipBuf* B(LuxBackendBuffer* b) { return reinterpret_cast<HipBuf*>(b); }
+
+double env_double(const char* name, double dflt) {
+    const char* v = getenv(name);
+    if (!v || !*v) return dflt;
+    char* end = nullptr;
+    double d = strtod(v, &end);
+    return (end && end != v && d >= 0.0) ? d : dflt;
+}
+
+// Bounded wait for the context stream (the counterpart of wgpu_wait_until,
+// src/webgpu_plugin.cpp:74-82): spin on hipStreamQuery, back off after 1 ms,
+// give up with DEVICE_LOST at the deadline.
+LuxBackendError wait_stream(HipCtx* c) {
+    const auto t0 = std::chrono::steady_clock::now();
+    const auto deadline = t0 + std::chrono::duration<double>(c->timeout_s);
+    for (;;) {
+        hipError_t e = hipStreamQuery(c->stream);
+        if (e == hipSuccess) return LUX_BACKEND_OK;
+        if (e != hipErrorNotReady)
+            return fail(LUX_BACKEND_ERROR_INTERNAL, "stream error: %s", hipGetErrorString(e));
+        auto now = std::chrono::steady_clock::now();
+        if (now > deadline)
+            return fail(LUX_BACKEND_ERROR_DEVICE_LOST, "wait exceeded %.3f s", c->timeout_s);
+        if (now - t0 > std::chrono::milliseconds(1))
+            std::this_thread::sleep_for(std::chrono::microseconds(50));
+    }
+}
+
+LuxBackendError begin_op(HipCtx* c, const char* op) {
+    if (!c->force_fail.empty() && c->force_fail == op)
+        return fail(LUX_BACKEND_ERROR_INTERNAL, "%s: forced failure (LUX_HIP_FORCE_FAIL)", op);
+    hipError_t e = hipSetDevice(c->device);
+    if (e != hipSuccess) return fail(LUX_BACKEND_ERROR_INTERNAL, "hipSetDevice: %s", hipGetErrorString(e));
+    return LUX_BACKEND_OK;
+}
+
+LuxBackendError end_op(HipCtx* c, hipError_t launch, const char* op) {
+    if (launch != hipSuccess)
+        return fail(LUX_BACKEND_ERROR_INTERNAL, "%s: launch failed: %s", op, hipGetErrorString(launch));
+    if (c->synchronous) return wait_stream(c);
+    return LUX_BACKEND_OK;
+}
+
+// ---------------------------------------------------------------- lifecycle
+LuxBackendContext* hip_create_context(int device_index) {
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n <= 0) {
+        fail(LUX_BACKEND_ERROR_NOT_SUPPORTED, "no HIP device");
+        return nullptr;
+    }
+    if (device_index < 0 || device_index >= n) {
+        fail(LUX_BACKEND_ERROR_INVALID_ARGUMENT, "device index %d out of range (%d)", device_index, n);
+        return nullptr;
+    }
+    auto* c = new HipCtx();
+    c->device = device_index;
+    if (hipSetDevice(device_index) != hipSuccess ||
+        hipGetDeviceProperties(&c->props, device_index) != hipSuccess ||
+        hipStreamCreateWithFlags(&c->own_stream, hipStreamNonBlocking) != hipSuccess) {
+        delete c;
+        fail(LUX_BACKEND_ERROR_INTERNAL, "HIP device %d initialisation failed", device_index);
+        return nullptr;
+    }
+    c->stream = c->own_stream;
+    c->timeout_s = env_double("LUX_HIP_WAIT_TIMEOUT_S", 5.0);
+    if (const char* f = getenv("LUX_HIP_FORCE_FAIL")) c->force_fail = f;
+    c->name = c->props.name[0] ? c->props.name : "AMD GPU";
+    c->name += " (";
+    c->name += c->props.gcnArchName;
+    c->name += ")";
+    return reinterpret_cast<LuxBackendContext*>(c);
+}
+
+void hip_destroy_context(LuxBackendContext* ctx) {
+    HipCtx* c = C(ctx);
+    if (!c) return;
+    (void)hipSetDevice(c->device);
+    if (c->own_stream) {
+        (void)hipStreamSynchronize(c->own_stream);
+        (void)hipStreamDestroy(c->own_stream);
+    }
+    delete c;
+}
+
+LuxBackendError hip_get_device_count(int* count) {
+    if (!count) return fail(LUX_BACKEND_ERROR_INVALID_ARGUMENT, "count is NULL");
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess) n = 0;
+    *count = n;
+    return LUX_BACKEND_OK;
+}
+
+LuxBackendError hip_get_device_info(LuxBackendContext* ctx, LuxBackendDeviceInfo* info) {
+    if (!info) return fail(LUX_BACKEND_ERROR_INVALID_ARGUMENT, "info is NULL");
+    HipCtx* c = C(ctx);
+    if (!c) return fail(LUX_BACKEND_ERROR_INTERNAL, "context is NULL");
+    size_t free_b = 0, total_b = 0;
+    (void)hipSetDevice(c->device);
+    if (hipMemGetInfo(&free_b, &total_b) != hipSuccess) {
+        free_b = c->props.totalGlobalMem;
+        total_b = c->props.totalGlobalMem;
+    }
+    info->name = c->name.c_str();
+    info->vendor = "AMD HIP";
+    info->memory_total = (uint64_t)total_b;
+    info->memory_available = (uint64_t)free_b;
+    info->compute_units = c->props.multiProcessorCount;
+    info->max_workgroup_size = c->props.maxThreadsPerBlock;
+    info->is_discrete = true;
+    info->is_unified_memory = false;
+    return LUX_BACKEND_OK;
+}
+
+LuxBackendError hip_sync(LuxBackendContext* ctx) {
+    HipCtx* c = C(ctx);
+    if (!c) return fail(LUX_BACKEND_ERROR_INTERNAL, "context is NULL");
+    if (hipSetDevice(c->device) != hipSuccess) return fail(LUX_BACKEND_ERROR_INTERNAL, "hipSetDevice");
+    return wait_stream(c);
+}
+
+// ---------------------------------------------------------------- buffers
+LuxBackendBuffer* hip_buffer_alloc(LuxBackendContext* ctx, size_t bytes) {
+    HipCtx* c = C(ctx);
+    if (!c) return nullptr;
+    (void)hipSetDevice(c->device);
+    auto* b = new HipBuf();
+    b->size = bytes;
+    b->device = c->device;
+    if (bytes > 0 && hipMalloc(&b->ptr, bytes) != hipSuccess) {
+        (void)hipGetLastError();
+        delete b;
+        fail(LUX_BACKEND_ERROR_OUT_OF_MEMORY, "hipMalloc(%zu) failed", bytes);
+        return nullptr;
+    }
+    return reinterpret_cast<LuxBackendBuffer*>(b);
+}
+
+LuxBackendError hip_buffer_copy_from_host(LuxBackendContext* ctx, LuxBackendBuffer* buf,
+                                          const void* src, size_t bytes);
+
+LuxBackendBuffer* hip_buffer_alloc_with_data(LuxBackendContext* ctx, const void* data, size_t bytes) {
+    LuxBackendBuffer* b = hip_buffer_alloc(ctx, bytes);
+    if (!b) return nullptr;
+    if (data && bytes && hip_buffer_copy_from_host(ctx, b, data, bytes) != LUX_BACKEND_OK) {
+        HipBuf* hb = B(b);
+        (void)hipFree(hb->ptr);
+        delete hb;
+        return nullptr;
+    }
+    return b;
+}
+
+void hip_buffer_free(LuxBackendContext* ctx, LuxBackendBuffer* buf) {
+    HipBuf* b = B(buf);
+    if (!b) return;
+    if (b->owned && b->ptr) {
+        (void)hipSetDevice(b->device);
+        if (HipCtx* c = C(ctx)) (void)hipStreamSynchronize(c->stream);
+        (void)hipFree(b->ptr);
+    }
+    delete b;
+}
+
+LuxBackendError hip_buffer_copy_to_host(LuxBackendContext* ctx, LuxBackendBuffer* buf, void* dst,
+                                        size_t bytes) {
+    HipCtx* c = C(ctx);
+    HipBuf* b = B(buf);
+    if (!c || !b || !dst) return fail(LUX_BACKEND_ERROR_INVALID_ARGUMENT, "copy_to_host: NULL argument");
+    size_t n = std::min(bytes, b->size);  // clamp, as src/webgpu_plugin.cpp:1495
+    if (n == 0) return LUX_BACKEND_OK;
+    if (LuxBackendError e = begin_op(c, "buffer_copy_to_host")) return e;
+    hipError_t he = hipMemcpyAsync(dst, b->ptr, n, hipMemcpyDeviceToHost, c->stream);
+    if (he != hipSuccess) return fail(LUX_BACKEND_ERROR_INTERNAL, "D2H copy: %s", hipGetErrorString(he));
+    return wait_stream(c);  // the host pointer must hold the data on return
+}
+
+LuxBackendError hip_buffer_copy_from_host(LuxBackendContext* ctx, LuxBackendBuffer* buf,
+                                          const void* src, size_t bytes) {
+    HipCtx* c = C(ctx);
+    HipBuf* b = B(buf);
+    if (!c || !b || !src) return fail(LUX_BACKEND_ERROR_INVALID_ARGUMENT, "copy_from_host: NULL argument");
+    size_t n = std::min(bytes, b->size);  // clamp, as src/webgpu_plugin.cpp:1553
+    if (n == 0) return LUX_BACKEND_OK;
+    if (LuxBackendError e = begin_op(c, "buffer_copy_from_host")) return e;
+    hipError_t he = hipMemcpyAsync(b->ptr, src, n, hipMemcpyHostToDevice, c->stream);
+    if (he != hipSuccess) return fail(LUX_BACKEND_ERROR_INTERNAL, "H2D copy: %s", hipGetErrorString(he));
+    return wait_stream(c);  // the caller may reuse src on return
+}
+
+void* hip_buffer_get_host_ptr(LuxBackendContext*, LuxBackendBuffer*) {
+    return nullptr;  // device memory is not host-visible (as src/webgpu_plugin.cpp:1564)
+}
+
+// ---------------------------------------------------------------- matmul
+bool fits(const HipBuf* b, size_t need) { return b && (need == 0 || (b->ptr && b->size >= need)); }
+
+LuxBackendError hip_op_matmul_f32(LuxBackendContext* ctx, LuxBackendBuffer* a, LuxBackendBuffer* b,
+                                  LuxBackendBuffer* out, int M, int K, int N) {
+    HipCtx* c = C(ctx);
+    HipBuf *A = B(a), *Bm = B(b), *O = B(out);
+    if (!c || !A || !Bm || !O) return fail(LUX_BACKEND_ERROR_INVALID_ARGUMENT, "matmul: NULL argument");
+    if (M < 0 || K < 0 || N < 0) return fail(LUX_BACKEND_ERROR_INVALID_ARGUMENT, "matmul: negative size");
+    const size_t m = M, k = K, n = N;
+    if (!fits(A, m * k * 4) || !fits(Bm, k * n * 4) || !fits(O, m * n * 4))
+        return fail(LUX_BACKEND_ERROR_INVALID_ARGUMENT, "matmul: buffer smaller than M*K/K*N/M*N floats");
+    if (LuxBackendError e = begin_op(c, "op_matmul_f32")) return e;
+    if (M == 0 || N == 0) return LUX_BACKEND_OK;
+    const float* pa = static_cast<const float*>(A->ptr);
+    const float* pb = static_cast<const float*>(Bm->ptr);
+    float* po = static_cast<float*>(O->ptr);
+    hipError_t he;
+    if (K == 0) {
+        he = hipMemsetAsync(po, 0, m * n * 4, c->stream);
+    } else if (N == 1) {
+        // GEMV: C[M] = A[M x K] . B[K]  (the reference runs this through the 16x16
+        // GEMM with 15/16 lanes idle, src/webgpu_plugin.cpp:1759-1763).
+        he = launch_gemv_f32(pa, pb, po, M, K, K, 1.0f, 0.0f, c->stream);
+    } else if (M == 1) {
+        // Row vector: C[N] = B^T[N x K] . a[K].
+        he = launch_gemv_f32_t(pb, pa, po, K, N, N, 1.0f, 0.0f, c->stream);
+    } else {
+        he = launch_gemm_f32(pa, pb, po, M, K, N, c->stream);
+    }
+    return end_op(c, he, "op_matmul_f32");
+}
+
+// ---------------------------------------------------------------- vtable
+const lux_gpu_backend_vtbl g_vtbl = [] {
+    lux_gpu_backend_vtbl v;
+    std::memset(&v, 0, sizeof v);  // every slot not named below stays NULL -> CPU fallback
+    v.create_context = hip_create_context;
+    v.destroy_context = hip_destroy_context;
+    v.get_device_count = hip_get_device_count;
+    v.get_device_info = hip_get_device_info;
+    v.sync = hip_sync;
+    v.buffer_alloc = hip_buffer_alloc;
+    v.buffer_alloc_with_data = hip_buffer_alloc_with_data;
+    v.buffer_free = hip_buffer_free;
+    v.buffer_copy_to_host = hip_buffer_copy_to_host;
+    v.buffer_copy_from_host = hip_buffer_copy_from_host;
+    v.buffer_get_host_ptr = hip_buffer_get_host_ptr;
+    v.op_matmul_f32 = hip_op_matmul_f32;
+    return v;
+}();
+
+// ---------------------------------------------------------------- quantized
+size_t dtype_bytes(int dt) {
+    switch (dt) {
+        case LUX_HIP_F32: case LUX_HIP_I32: return 4;
+        case LUX_HIP_F16: case LUX_HIP_BF16: return 2;
+        case LUX_HIP_I8: return 1;
+        default: return 0;
+    }
+}
+
+size_t scale_bytes(int fmt) {
+    switch (fmt) {
+        case LUX_HIP_SCALE_F16: return 2;
+        case LUX_HIP_SCALE_F32: return 4;
+        case LUX_HIP_SCALE_GROUPSCALE: return 16;
+        default: return 0;
+    }
+}
+
+}  // namespace
+
+// ============================================================== exports
+LUX_EXPORT bool lux_gpu_backend_init(lux_gpu_backend_desc* out) {
+    if (!out) return false;
+    out->abi_version = LUX_GPU_BACKEND_ABI_VERSION;
+    out->vtbl_size = (uint32_t)sizeof(lux_gpu_backend_vtbl);
+    out->backend_name = "hip";
+    out->backend_version = "0.1.0";
+    out->capabilities = LUX_CAP_TENSOR_OPS | LUX_CAP_MATMUL;
+    out->vtbl = &g_vtbl;
+    return true;
+}
+
+LUX_EXPORT uint32_t lux_hip_quant_api_version(void) { return LUX_HIP_QUANT_API_VERSION; }
+
+LUX_EXPORT const char* lux_hip_last_error(void) { return g_last_error.c_str(); }
+
+LUX_EXPORT LuxBackendBuffer* lux_hip_buffer_wrap(LuxBackendContext* ctx, void* device_ptr, size_t bytes) {
+    HipCtx* c = C(ctx);
+    if (!c || (!device_ptr && bytes)) {
+        fail(LUX_BACKEND_ERROR_INVALID_ARGUMENT, "buffer_wrap: NULL argument");
+        return nullptr;
+    }
+    auto* b = new HipBuf();
+    b->ptr = device_ptr;
+    b->size = bytes;
+    b->owned = false;
+    b->device = c->device;
+    return reinterpret_cast<LuxBackendBuffer*>(b);
+}
+
+LUX_EXPORT void* lux_hip_buffer_device_ptr(LuxBackendBuffer* buf) { return buf ? B(buf)->ptr : nullptr; }
+LUX_EXPORT size_t lux_hip_buffer_size(LuxBackendBuffer* buf) { return buf ? B(buf)->size : 0; }
+
+LUX_EXPORT LuxBackendError lux_hip_context_set_stream(LuxBackendContext* ctx, void* stream) {
+    HipCtx* c = C(ctx);
+    if (!c) return fail(LUX_BACKEND_ERROR_INVALID_ARGUMENT, "set_stream: NULL context");
+    c->stream = stream ? static_cast<hipStream_t>(stream) : c->own_stream;
+    return LUX_BACKEND_OK;
+}
+
+LUX_EXPORT void* lux_hip_context_get_stream(LuxBackendContext* ctx) {
+    HipCtx* c = C(ctx);
+    return c ? static_cast<void*>(c->stream) : nullptr;
+}
+
+LUX_EXPORT LuxBackendError lux_hip_context_set_synchronous(LuxBackendContext* ctx, int synchronous) {
+    HipCtx* c = C(ctx);
+    if (!c) return fail(LUX_BACKEND_ERROR_INVALID_ARGUMENT, "set_synchronous: NULL context");
+    c->synchronous = synchronous != 0;
+    return LUX_BACKEND_OK;
+}
+
+LUX_EXPORT LuxBackendError lux_hip_gemv_f32(LuxBackendContext* ctx, LuxBackendBuffer* a,
+                                            LuxBackendBuffer* x, LuxBackendBuffer* y,
+                                            const LuxHipGemvParams* p) {
+    HipCtx* c = C(ctx);
+    HipBuf *A = B(a), *X = B(x), *Y = B(y);
+    if (!c || !A || !X || !Y || !p) return fail(LUX_BACKEND_ERROR_INVALID_ARGUMENT, "gemv_f32: NULL argument");
+    const size_t M = p->M, N = p->N, lda = p->lda;
+    if (lda < N || M > INT32_MAX || N > INT32_MAX || lda > INT32_MAX)
+        return fail(LUX_BACKEND_ERROR_INVALID_ARGUMENT, "gemv_f32: lda < N or size too large");
+    const size_t a_need = M ? ((M - 1) * lda + N) * 4 : 0;
+    const size_t x_need = (p->trans ? M : N) * 4, y_need = (p->trans ? N : M) * 4;
+    if (!fits(A, a_need) || !fits(X, x_need) || !fits(Y, y_need))
+        return fail(LUX_BACKEND_ERROR_INVALID_ARGUMENT, "gemv_f32: buffer too small");
+    if (LuxBackendError e = begin_op(c, "gemv_f32")) return e;
+    const size_t outn = p->trans ? N : M;
+    if (outn == 0) return LUX_BACKEND_OK;
+    hipError_t he;
+    if (p->trans)
+        he = launch_gemv_f32_t((const float*)A->ptr, (const float*)X->ptr, (float*)Y->ptr, (int)M, (int)N,
+                               (int)lda, p->alpha, p->beta, c->stream);
+    else
+        he = launch_gemv_f32((const float*)A->ptr, (const float*)X->ptr, (float*)Y->ptr, (int)M, (int)N,
+                             (int)lda, p->alpha, p->beta, c->stream);
+    return end_op(c, he, "gemv_f32");
+}
+
+LUX_EXPORT LuxBackendError lux_hip_gemv_f16(LuxBackendContext* ctx, LuxBackendBuffer* a,
+                                            LuxBackendBuffer* x, LuxBackendBuffer* y, uint32_t M,
+                                            uint32_t N, uint32_t lda) {
+    HipCtx* c = C(ctx);
+    HipBuf *A = B(a), *X = B(x), *Y = B(y);
+    if (!c || !A || !X || !Y) return fail(LUX_BACKEND_ERROR_INVALID_ARGUMENT, "gemv_f16: NULL argument");
+    if (lda < N || M > INT32_MAX || lda > INT32_MAX)
+        return fail(LUX_BACKEND_ERROR_INVALID_ARGUMENT, "gemv_f16: lda < N or size too large");
+    const size_t a_need = M ? (((size_t)M - 1) * lda + N) * 2 : 0;
+    if (!fits(A, a_need) || !fits(X, (size_t)N * 2) || !fits(Y, (size_t)M * 4))
+        return fail(LUX_BACKEND_ERROR_INVALID_ARGUMENT, "gemv_f16: buffer too small");
+    if (LuxBackendError e = begin_op(c, "gemv_f16")) return e;
+    if (M == 0) return LUX_BACKEND_OK;
+    hipError_t he = launch_gemv_f16(A->ptr, X->ptr, (float*)Y->ptr, (int)M, (int)N, (int)lda, c->stream);
+    return end_op(c, he, "gemv_f16");
+}
+
+LUX_EXPORT LuxBackendError lux_hip_qmatmul(LuxBackendContext* ctx, const LuxHipQMatmulDesc* d,
+                                           LuxBackendBuffer* w, LuxBackendBuffer* w_scales,
+                                           LuxBackendBuffer* x, LuxBackendBuffer* x_scales,
+                                           LuxBackendBuffer* y) {
+    HipCtx* c = C(ctx);
+    if (!c || !d || !w || !x || !y) return fail(LUX_BACKEND_ERROR_INVALID_ARGUMENT, "qmatmul: NULL argument");
+    if (d->struct_size < sizeof(LuxHipQMatmulDesc))
+        return fail(LUX_BACKEND_ERROR_INVALID_ARGUMENT, "qmatmul: struct_size %u too small", d->struct_size);
+    const int n_out = d->n_out, K = d->k, M = d->m, gs = d->group_size;
+    if (n_out < 0 || K < 0 || M < 0) return fail(LUX_BACKEND_ERROR_INVALID_ARGUMENT, "qmatmul: negative size");
+    if (d->weight_bits != 4 && d->weight_bits != 8)
+        return fail(LUX_BACKEND_ERROR_INVALID_ARGUMENT, "qmatmul: weight_bits must be 4 or 8");
+    if (K % 32 != 0) return fail(LUX_BACKEND_ERROR_NOT_SUPPORTED, "qmatmul: k %% 32 != 0");
+    const bool w4a8 = d->x_dtype == LUX_HIP_I8;
+    const bool no_scale = d->scale_format == LUX_HIP_SCALE_NONE;
+    if (!no_scale && (gs <= 0 || K % gs != 0 || gs % 8 != 0))
+        return fail(LUX_BACKEND_ERROR_INVALID_ARGUMENT, "qmatmul: group_size %d must divide k and be a multiple of 8", gs);
+    if (d->nibble_coding != LUX_HIP_NIBBLE_OFFSET_BINARY && d->nibble_coding != LUX_HIP_NIBBLE_TWOS_COMPLEMENT)
+        return fail(LUX_BACKEND_ERROR_INVALID_ARGUMENT, "qmatmul: bad nibble_coding");
+    const size_t xb = dtype_bytes(d->x_dtype), yb = dtype_bytes(d->y_dtype);
+    if (!xb || !yb || (d->x_dtype == LUX_HIP_I32) || (!w4a8 && d->y_dtype == LUX_HIP_I32))
+        return fail(LUX_BACKEND_ERROR_NOT_SUPPORTED, "qmatmul: dtype combination");
+    if (scale_bytes(d->scale_format) == 0 && !no_scale)
+        return fail(LUX_BACKEND_ERROR_INVALID_ARGUMENT, "qmatmul: bad scale_format");
+    const bool partials = (d->flags & LUX_HIP_QFLAG_GROUP_PARTIALS) != 0;
+    if (partials && !(w4a8 && d->y_dtype == LUX_HIP_I32 && !no_scale))
+        return fail(LUX_BACKEND_ERROR_INVALID_ARGUMENT, "qmatmul: GROUP_PARTIALS needs W4A8, I32 out and a group_size");
+
+    const size_t wn = (size_t)n_out * K * d->weight_bits / 8;
+    const size_t groups = no_scale ? 0 : (size_t)n_out * (K / gs);
+    const size_t yn = partials ? (size_t)M * n_out * (K / gs) * 4 : (size_t)M * n_out * yb;
+    HipBuf *W = B(w), *S = B(w_scales), *X = B(x), *XS = B(x_scales), *Y = B(y);
+    if (!fits(W, wn) || !fits(X, (size_t)M * K * xb) || !fits(Y, yn))
+        return fail(LUX_BACKEND_ERROR_INVALID_ARGUMENT, "qmatmul: weight/activation/output buffer too small");
+    if (!no_scale && !fits(S, groups * scale_bytes(d->scale_format)))
+        return fail(LUX_BACKEND_ERROR_INVALID_ARGUMENT, "qmatmul: scale buffer too small");
+    const bool need_xs = w4a8 && d->y_dtype != LUX_HIP_I32;
+    if (need_xs && !fits(XS, (size_t)M * 4))
+        return fail(LUX_BACKEND_ERROR_INVALID_ARGUMENT, "qmatmul: x_scales (f32 [m]) required for W4A8 fp output");
+
+    if (LuxBackendError e = begin_op(c, "qmatmul")) return e;
+    if (M == 0 || n_out == 0) return LUX_BACKEND_OK;
+
+    QArgs a{};
+    a.w = W->ptr;
+    a.s = no_scale ? nullptr : S->ptr;
+    a.x = X->ptr;
+    a.xs = need_xs ? static_cast<const float*>(XS->ptr) : nullptr;
+    a.y = Y->ptr;
+    a.n_out = n_out;
+    a.k = K;
+    a.m = M;
+    a.group_size = no_scale ? K : gs;
+    a.wbits = d->weight_bits;
+    a.scale_kind = static_cast<ScaleKind>(d->scale_format);
+    a.x_kind = static_cast<XKind>(d->x_dtype);
+    a.y_kind = static_cast<YKind>(d->y_dtype);
+    a.group_partials = partials;
+    // Kernels decode offset-binary nibbles; two's complement becomes offset-binary
+    // with one xor per word (ob = tc ^ 0x8, quantized.wgsl:152 vs quantized_nax.wgsl:109).
+    a.xor_mask = (d->weight_bits == 4 && d->nibble_coding == LUX_HIP_NIBBLE_TWOS_COMPLEMENT) ? 0x88888888u : 0u;
+
+    hipError_t he;
+    if (w4a8) {
+        if (d->weight_bits != 4 || !w4a8_supported(a))
+            return fail(LUX_BACKEND_ERROR_NOT_SUPPORTED, "qmatmul: W4A8 shape/format not supported");
+        he = launch_w4a8(a, c->stream);
+    } else if (d->weight_bits == 4 && M == 1) {
+        he = launch_qgemv_i4(a, c->stream);
+    } else if (d->weight_bits == 4 && qgemm_i4_large_supported(a)) {
+        he = launch_qgemm_i4_large(a, c->stream);
+    } else if (qgemm_small_supported(a)) {
+        he = launch_qgemm_small(a, c->stream);
+    } else {
+        return fail(LUX_BACKEND_ERROR_NOT_SUPPORTED, "qmatmul: no kernel for this descriptor");
+    }
+    return end_op(c, he, "qmatmul");
+}

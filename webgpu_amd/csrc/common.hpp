@@ -50,6 +50,21 @@ __device__ __forceinline__ float load_scale_t(const void* s, size_t idx) {
     else return 1.0f;
 }
 
+// Raw scale bits, converted only where used (keeps the load off the critical path).
+template <ScaleKind K>
+__device__ __forceinline__ uint32_t load_scale_raw(const void* s, size_t idx) {
+    if constexpr (K == ScaleKind::F16) return reinterpret_cast<const uint16_t*>(s)[idx];
+    else if constexpr (K == ScaleKind::F32) return reinterpret_cast<const uint32_t*>(s)[idx];
+    else if constexpr (K == ScaleKind::GroupScale) return reinterpret_cast<const uint32_t*>(s)[4 * idx];
+    else return 0x3F800000u;
+}
+
+template <ScaleKind K>
+__device__ __forceinline__ float scale_from_raw(uint32_t b) {
+    if constexpr (K == ScaleKind::F16) return (float)__builtin_bit_cast(f16, (uint16_t)b);
+    else return __builtin_bit_cast(float, b);
+}
+
 __device__ __forceinline__ float bf16_bits_to_f32(uint32_t b) {
     return __builtin_bit_cast(float, b << 16);
 }

@@ -12,102 +12,133 @@
 //   - lane l of a wave owns slices l, l+64, ... of every row, so its slice of x is
 //     loop-invariant and lives in registers, pre-permuted into the (k, k+4) fp16
 //     pairs the nibble decode produces;
-//   - nibbles become fp16 with the 0x6400 exponent trick (1024 + n, or 1024 + 16n
-//     for the odd nibbles), one v_pk_add_f16 removes the offset exactly, and
-//     v_dot2_f32_f16 accumulates exact products in fp32;
-//   - each wave handles RPW rows with all RPW*SPL loads issued before any math.
+//   - a masked nibble pair is read directly as two fp16 subnormals (n * 2^-24),
+//     v_dot2_f32_f16 accumulates the exact products n*x in fp32, and the offset
+//     of the offset-binary code is removed once per slice as -8 * sum(x);
+//   - each wave owns a run of rows and issues all their loads before any math.
 #include "common.hpp"
 
 namespace luxhip {
 
 __device__ __forceinline__ f16x2 as_h2(uint32_t v) { return __builtin_bit_cast(f16x2, v); }
 
-// sum_{i<32} (nib_i - 8) * x_i for one 16-byte slice.
-__device__ __forceinline__ float dot_slice_f16(const uint32_t (&q)[4], const f16x2 (&xp)[4][4]) {
-    const uint32_t MAGIC = 0x64006400u;
-    const f16x2 OFF1 = {(f16)1032.0f, (f16)1032.0f};  // 1024 + 8
-    const f16x2 OFF16 = {(f16)1152.0f, (f16)1152.0f}; // 1024 + 16*8
+// sum_{i<32} nib_i * x_i * 2^-24 for one 16-byte slice.  A masked nibble read as
+// an fp16 bit pattern is the subnormal n * 2^-24 (no implicit bit, no offset to
+// remove), so decode is one AND per pair; v_dot2_f32_f16 multiplies exactly
+// (f16 denormals are preserved) and accumulates in fp32.  The odd nibbles are
+// masked in place (16n * 2^-24) and rescaled by 1/16 at the end.  9 VALU ops
+// per 8 weights.
+__device__ __forceinline__ float dot_slice_sub(const uint32_t (&q)[4], const f16x2 (&xp)[4][4]) {
     float lo = 0.f, hi = 0.f;
 #pragma unroll
     for (int w = 0; w < 4; ++w) {
         const uint32_t word = q[w];
         const uint32_t w8 = word >> 8;
-        f16x2 v0 = as_h2((word & 0x000F000Fu) | MAGIC) - OFF1;   // (n0, n4) - 8
-        f16x2 v1 = as_h2((word & 0x00F000F0u) | MAGIC) - OFF16;  // 16*((n1, n5) - 8)
-        f16x2 v2 = as_h2((w8 & 0x000F000Fu) | MAGIC) - OFF1;     // (n2, n6) - 8
-        f16x2 v3 = as_h2((w8 & 0x00F000F0u) | MAGIC) - OFF16;    // 16*((n3, n7) - 8)
-        lo = __builtin_amdgcn_fdot2(v0, xp[w][0], lo, false);
-        hi = __builtin_amdgcn_fdot2(v1, xp[w][1], hi, false);
-        lo = __builtin_amdgcn_fdot2(v2, xp[w][2], lo, false);
-        hi = __builtin_amdgcn_fdot2(v3, xp[w][3], hi, false);
+        lo = __builtin_amdgcn_fdot2(as_h2(word & 0x000F000Fu), xp[w][0], lo, false);  // n0, n4
+        hi = __builtin_amdgcn_fdot2(as_h2(word & 0x00F000F0u), xp[w][1], hi, false);  // 16 n1, 16 n5
+        lo = __builtin_amdgcn_fdot2(as_h2(w8 & 0x000F000Fu), xp[w][2], lo, false);    // n2, n6
+        hi = __builtin_amdgcn_fdot2(as_h2(w8 & 0x00F000F0u), xp[w][3], hi, false);    // 16 n3, 16 n7
     }
     return fmaf(hi, 0.0625f, lo);
 }
 
-template <int SPL, int RPW, ScaleKind SK, YKind YK>
+// One wave owns RW consecutive rows (the last wave may own fewer).  It issues every load it will
+// need up front -- x slice, all rows' weight slices, all scales -- and then
+// consumes rows in order, so the math of row r overlaps the loads of rows > r.
+// The host sizes the grid to 8 waves per CU with equal rows per wave.
+template <int SPL, int RW, ScaleKind SK, YKind YK, bool XOR>
 __global__ __launch_bounds__(256) void k_qgemv_i4_f16(const u32x4* __restrict__ W,
                                                       const void* __restrict__ S,
                                                       const f16* __restrict__ x,
                                                       void* __restrict__ y, int n_out, int K,
                                                       int spg, uint32_t xor_mask) {
     const int lane = threadIdx.x & 63;
-    const int row0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * RPW;
+    const int row0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * RW;
     if (row0 >= n_out) return;
+    const int nrows = min(RW, n_out - row0);
     const int s_row = K >> 5;        // slices per row
     const int g_row = s_row / spg;   // groups per row
 
-    f16x2 xp[SPL][4][4];
-    int gid[SPL];
-    bool ok[SPL];
+    // Load order matters: vmcnt retires loads in issue order, so x (an L2 hit)
+    // goes first, then every weight slice and raw scale of the wave's rows.  All
+    // addresses are clamped to valid ones; out-of-range slices get x = 0 after
+    // the loads, and rows past the wave's share are never computed or stored.
+    u32x4 xr[SPL][4];
+    int sl[SPL];
 #pragma unroll
     for (int j = 0; j < SPL; ++j) {
-        const int s = lane + 64 * j;
-        ok[j] = s < s_row;
-        gid[j] = s / spg;
-        const f16x8* x8 = reinterpret_cast<const f16x8*>(x) + 4 * s;
+        sl[j] = min(lane + 64 * j, s_row - 1);
+        const u32x4* x8 = reinterpret_cast<const u32x4*>(x) + 4 * sl[j];
+#pragma unroll
+        for (int w = 0; w < 4; ++w) xr[j][w] = x8[w];
+    }
+    __builtin_amdgcn_sched_barrier(0);  // keep x loads ahead of the weight stream
+
+    u32x4 q[RW][SPL];
+    uint32_t sraw[RW][SPL];
+#pragma unroll
+    for (int r = 0; r < RW; ++r) {
+        // Straight-line loads (no branch) keep the waitcnt bookkeeping exact.  In the
+        // last wave, rows past n_out read the last matrix row instead (an L2 hit) and
+        // are computed but never stored.
+        {
+            const size_t row = (size_t)min(row0 + r, n_out - 1);
+#pragma unroll
+            for (int j = 0; j < SPL; ++j) {
+                q[r][j] = __builtin_nontemporal_load(W + row * s_row + sl[j]);
+                if constexpr (SK == ScaleKind::F16)  // aligned u32 holding this scale (g_row is even)
+                    sraw[r][j] = reinterpret_cast<const uint32_t*>(S)[(row * g_row + sl[j] / spg) >> 1];
+                else
+                    sraw[r][j] = load_scale_raw<SK>(S, row * g_row + sl[j] / spg);
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);  // rows issue in order: row r arrives first
+    }
+
+    __builtin_amdgcn_sched_barrier(0);  // all loads are in flight before any math
+
+    // x pairs in decode order and, per slice, -8 * sum(x) (offset-binary q = n - 8).
+    f16x2 xp[SPL][4][4];
+    float xoff[SPL];
+    const f16x2 ONES = {(f16)1.0f, (f16)1.0f};
+#pragma unroll
+    for (int j = 0; j < SPL; ++j) {
+        const uint32_t keep = lane + 64 * j < s_row ? ~0u : 0u;  // bitwise: no branch
+        float sx = 0.f;
 #pragma unroll
         for (int w = 0; w < 4; ++w) {
-            f16x8 v = ok[j] ? x8[w] : f16x8{};
+            const u32x4 u = xr[j][w] & keep;
+            const f16x8 v = __builtin_bit_cast(f16x8, u);
             xp[j][w][0] = f16x2{v[0], v[4]};
             xp[j][w][1] = f16x2{v[1], v[5]};
             xp[j][w][2] = f16x2{v[2], v[6]};
             xp[j][w][3] = f16x2{v[3], v[7]};
+#pragma unroll
+            for (int p = 0; p < 4; ++p) sx = __builtin_amdgcn_fdot2(xp[j][w][p], ONES, sx, false);
         }
+        xoff[j] = -8.0f * sx;
     }
 
-    uint32_t q[RPW][SPL][4];
-    float sc[RPW][SPL];
+    float res = 0.f;
 #pragma unroll
-    for (int r = 0; r < RPW; ++r)
+    for (int r = 0; r < RW; ++r) {
+        float acc = 0.f;
 #pragma unroll
         for (int j = 0; j < SPL; ++j) {
-            const int row = row0 + r;
-            if (row < n_out && ok[j]) {
-                u32x4 v = __builtin_nontemporal_load(W + (size_t)row * s_row + lane + 64 * j);
-                q[r][j][0] = v.x ^ xor_mask; q[r][j][1] = v.y ^ xor_mask;
-                q[r][j][2] = v.z ^ xor_mask; q[r][j][3] = v.w ^ xor_mask;
-                sc[r][j] = load_scale_t<SK>(S, (size_t)row * g_row + gid[j]);
-            } else {
-                q[r][j][0] = q[r][j][1] = q[r][j][2] = q[r][j][3] = 0x88888888u;  // q = 0
-                sc[r][j] = 0.f;
+            uint32_t sb = sraw[r][j];
+            if constexpr (SK == ScaleKind::F16) sb = (sb >> (((sl[j] / spg) & 1) * 16)) & 0xFFFFu;
+            uint32_t qq[4] = {q[r][j].x, q[r][j].y, q[r][j].z, q[r][j].w};
+            if constexpr (XOR) {
+#pragma unroll
+                for (int w = 0; w < 4; ++w) qq[w] ^= xor_mask;
             }
+            const float part = fmaf(dot_slice_sub(qq, xp[j]), 16777216.0f, xoff[j]);  // * 2^24
+            acc = fmaf(part, scale_from_raw<SK>(sb), acc);
         }
-
-    float acc[RPW];
-#pragma unroll
-    for (int r = 0; r < RPW; ++r) {
-        acc[r] = 0.f;
-#pragma unroll
-        for (int j = 0; j < SPL; ++j) acc[r] = fmaf(dot_slice_f16(q[r][j], xp[j]), sc[r][j], acc[r]);
+        acc = wave_sum(acc);
+        res = lane == r ? acc : res;
     }
-#pragma unroll
-    for (int r = 0; r < RPW; ++r) acc[r] = wave_sum(acc[r]);
-    if (lane < RPW) {
-        float v = acc[0];
-#pragma unroll
-        for (int r = 1; r < RPW; ++r) v = lane == r ? acc[r] : v;
-        if (row0 + lane < n_out) store_y<YK>(y, row0 + lane, v);
-    }
+    if (lane < nrows) store_y<YK>(y, row0 + lane, res);
 }
 
 // Any activation dtype, any group size that is a multiple of 8: one wave per row,
@@ -135,14 +166,52 @@ __global__ __launch_bounds__(256) void k_qgemv_i4_generic(const uint32_t* __rest
     if (lane == 0) store_y<YK>(y, row, acc);
 }
 
+static int device_cus() {
+    static int cus[64] = {0};
+    int dev = 0;
+    (void)hipGetDevice(&dev);
+    if (dev < 0 || dev >= 64) return 256;
+    if (!cus[dev]) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+        cus[dev] = n;
+    }
+    return cus[dev];
+}
+
+template <int SPL, int RW, ScaleKind SK, YKind YK>
+static void launch_rw(const QArgs& a, hipStream_t s) {
+    const int waves = (a.n_out + RW - 1) / RW;
+    const dim3 grid((waves + 3) / 4), block(256);
+    const u32x4* w = reinterpret_cast<const u32x4*>(a.w);
+    const f16* x = reinterpret_cast<const f16*>(a.x);
+    if (a.xor_mask)
+        hipLaunchKernelGGL((k_qgemv_i4_f16<SPL, RW, SK, YK, true>), grid, block, 0, s, w, a.s, x,
+                           a.y, a.n_out, a.k, a.group_size / 32, a.xor_mask);
+    else
+        hipLaunchKernelGGL((k_qgemv_i4_f16<SPL, RW, SK, YK, false>), grid, block, 0, s, w, a.s, x,
+                           a.y, a.n_out, a.k, a.group_size / 32, a.xor_mask);
+}
+
+// Rows per wave: enough for 8 waves per CU with equal shares (14336 rows on 256
+// CUs -> 7 rows per wave, 2048 waves); capped so the weight registers
+// (RW * SPL * 4 VGPRs) stay within 64.
 template <int SPL, ScaleKind SK, YKind YK>
 static void launch_fast(const QArgs& a, hipStream_t s) {
-    constexpr int RPW = 4;
-    const int waves = (a.n_out + RPW - 1) / RPW;
-    hipLaunchKernelGGL((k_qgemv_i4_f16<SPL, RPW, SK, YK>), dim3((waves + 3) / 4), dim3(256), 0, s,
-                       reinterpret_cast<const u32x4*>(a.w), a.s,
-                       reinterpret_cast<const f16*>(a.x), a.y, a.n_out, a.k, a.group_size / 32,
-                       a.xor_mask);
+    constexpr int RWMAX = SPL <= 2 ? 8 : 16 / SPL;
+    const int target_waves = device_cus() * 8;
+    int rw = (a.n_out + target_waves - 1) / target_waves;
+    rw = rw < 1 ? 1 : (rw > RWMAX ? RWMAX : rw);
+    switch (rw) {
+        case 1: launch_rw<SPL, 1, SK, YK>(a, s); break;
+        case 2: launch_rw<SPL, 2, SK, YK>(a, s); break;
+        case 3: if constexpr (RWMAX >= 3) launch_rw<SPL, 3, SK, YK>(a, s); break;
+        case 4: if constexpr (RWMAX >= 4) launch_rw<SPL, 4, SK, YK>(a, s); break;
+        case 5: if constexpr (RWMAX >= 5) launch_rw<SPL, 5, SK, YK>(a, s); break;
+        case 6: if constexpr (RWMAX >= 6) launch_rw<SPL, 6, SK, YK>(a, s); break;
+        case 7: if constexpr (RWMAX >= 7) launch_rw<SPL, 7, SK, YK>(a, s); break;
+        default: if constexpr (RWMAX >= 8) launch_rw<SPL, 8, SK, YK>(a, s); break;
+    }
 }
 
 template <ScaleKind SK, YKind YK>
@@ -190,6 +259,7 @@ static bool launch_generic(const QArgs& a, hipStream_t s) {
 
 hipError_t launch_qgemv_i4(const QArgs& a, hipStream_t s) {
     const bool fast = a.x_kind == XKind::F16 && a.k % 32 == 0 && a.group_size % 32 == 0 &&
+                      (a.scale_kind != ScaleKind::F16 || (a.k / a.group_size) % 2 == 0) &&
                       ((uintptr_t)a.w & 15u) == 0 && ((uintptr_t)a.x & 15u) == 0;
     bool launched = false;
     if (fast) {

@@ -1,0 +1,105 @@
+"""GPU parity: weight-only quantized GEMM (m > 1) through lux_hip_qmatmul.
+
+Oracle: matmul_nax_grouped (quantized_nax.wgsl:568-626) and the int8
+dequantize + matmul composition (quantized_nax.wgsl:364-386 +
+src/webgpu_plugin.cpp:138-205), restated in oracle/lux_oracle.c and evaluated in
+the reference layout (act = X^T, out = Y^T).  Tolerance for every fp path:
+rel-L2 <= 1e-3 and max-abs <= 1e-2 * ||ref||_inf against the oracle rounded (RNE)
+to the output dtype.
+"""
+import numpy as np
+import pytest
+
+import oracle
+import webgpu_amd as W
+from util import bf16_bits, bf16_to_f32, compare, int4_weights, int8_weights, rng, round_to
+
+pytestmark = pytest.mark.gpu
+
+YD = {"f16": (W.F16, np.float16), "f32": (W.F32, np.float32), "bf16": (W.BF16, np.uint16)}
+
+
+def _run(ctx, desc, Wp, s, X, n_out, m, y):
+    ycode, ynp = YD[y]
+    wb, sb, xb = ctx.upload(Wp), ctx.upload(s), ctx.upload(X)
+    yb = ctx.alloc(m * n_out * np.dtype(ynp).itemsize)
+    ctx.qmatmul(desc, wb, sb, xb, None, yb)
+    out = ctx.download(yb, ynp, (m, n_out))
+    if y == "bf16":
+        out = bf16_to_f32(out)
+    return out.astype(np.float64)
+
+
+def _x(r, m, K, xd):
+    xf = r.standard_normal((m, K)).astype(np.float32)
+    if xd == "bf16":
+        b = bf16_bits(xf)
+        return b, bf16_to_f32(b), W.BF16
+    h = xf.astype(np.float16)
+    return h, h.astype(np.float32), W.F16
+
+
+def test_config4_full(ctx):
+    """C4: X 2048 x 4096 bf16 N(0,1), W 14336 x 4096 int4 g32 fp16 scales, bf16 out."""
+    r = rng(4)
+    n_out, K, m, gs = 14336, 4096, 2048, 32
+    q, Wp, s = int4_weights(r, n_out, K, gs)
+    X, Xf, xc = _x(r, m, K, "bf16")
+    d = W.qdesc(n_out, K, m, 4, gs, W.NIBBLE_OFFSET_BINARY, W.SCALE_F16, xc, W.BF16)
+    got = _run(ctx, d, Wp, s, X, n_out, m, "bf16")
+    ref = oracle.matmul_nax_grouped_tokens(Wp, s.astype(np.float32).reshape(-1), Xf, gs)
+    st = compare(got, round_to(ref, "bf16"), "C4 full")
+    print(f"C4 rel-L2 {st['rel_l2']:.3e} max-abs/inf {st['max_abs'] / st['ref_inf']:.3e}")
+
+
+@pytest.mark.parametrize("n_out,K,m,gs,xd,y", [
+    (256, 64, 2, 32, "bf16", "f32"),
+    (300, 128, 5, 32, "f16", "f32"),
+    (520, 512, 33, 128, "bf16", "bf16"),
+    (256, 1024, 300, 64, "f16", "f16"),
+    (1000, 256, 257, 32, "bf16", "f32"),
+])
+def test_int4_gemm_shapes(ctx, n_out, K, m, gs, xd, y):
+    r = rng(n_out + K + m)
+    q, Wp, s = int4_weights(r, n_out, K, gs)
+    X, Xf, xc = _x(r, m, K, xd)
+    d = W.qdesc(n_out, K, m, 4, gs, W.NIBBLE_OFFSET_BINARY, W.SCALE_F16, xc, YD[y][0])
+    got = _run(ctx, d, Wp, s, X, n_out, m, y)
+    ref = oracle.matmul_nax_grouped_tokens(Wp, s.astype(np.float32).reshape(-1), Xf, gs)
+    compare(got, round_to(ref, y), f"gemm {n_out}x{K} m{m} g{gs} {xd}->{y}")
+
+
+@pytest.mark.parametrize("scale_fmt", [W.SCALE_F32, W.SCALE_GROUPSCALE])
+@pytest.mark.parametrize("coding", [0, 1])
+def test_int4_gemm_formats(ctx, scale_fmt, coding):
+    r = rng(40 + 2 * scale_fmt + coding)
+    n_out, K, m, gs = 384, 256, 70, 32
+    q, Wp, _ = int4_weights(r, n_out, K, gs, coding)
+    s32 = r.uniform(0.005, 0.02, size=(n_out, K // gs)).astype(np.float32)
+    if scale_fmt == W.SCALE_F32:
+        sbuf = s32
+    else:
+        sbuf = np.zeros(s32.shape + (4,), np.float32)
+        sbuf[..., 0] = s32
+    X, Xf, xc = _x(r, m, K, "bf16")
+    d = W.qdesc(n_out, K, m, 4, gs, coding, scale_fmt, xc, W.F32)
+    got = _run(ctx, d, Wp, sbuf, X, n_out, m, "f32")
+    ref = oracle.matmul_nax_grouped_tokens(Wp, s32.reshape(-1), Xf, gs, coding)
+    compare(got, ref, f"formats {scale_fmt} {coding}")
+
+
+def test_int4_gemm_exact_grid(ctx):
+    """Power-of-two scales and small-integer activations: every staged value and
+    product is exact, so the GPU result must equal the oracle bit-for-bit."""
+    r = rng(9)
+    n_out, K, m, gs = 512, 512, 64, 32
+    q = r.integers(-8, 8, size=(n_out, K))
+    from util import pack_nibbles
+    Wp = pack_nibbles(q, 0)
+    s = (2.0 ** r.integers(-6, 0, size=(n_out, K // gs))).astype(np.float16)
+    Xf = r.integers(-4, 5, size=(m, K)).astype(np.float32)
+    X = Xf.astype(np.float16)
+    d = W.qdesc(n_out, K, m, 4, gs, W.NIBBLE_OFFSET_BINARY, W.SCALE_F16, W.F16, W.F32)
+    got = _run(ctx, d, Wp, s, X, n_out, m, "f32")
+    ref = oracle.matmul_nax_grouped_tokens(Wp, s.astype(np.float32).reshape(-1), Xf, gs)
+    assert np.array_equal(got, ref.astype(np.float64))

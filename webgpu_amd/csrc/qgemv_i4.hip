@@ -16,6 +16,8 @@
 //     v_dot2_f32_f16 accumulates the exact products n*x in fp32, and the offset
 //     of the offset-binary code is removed once per slice as -8 * sum(x);
 //   - each wave owns a run of rows and issues all their loads before any math.
+#include <cstdlib>
+
 #include "common.hpp"
 
 namespace luxhip {
@@ -46,7 +48,7 @@ __device__ __forceinline__ float dot_slice_sub(const uint32_t (&q)[4], const f16
 // need up front -- x slice, all rows' weight slices, all scales -- and then
 // consumes rows in order, so the math of row r overlaps the loads of rows > r.
 // The host sizes the grid to 8 waves per CU with equal rows per wave.
-template <int SPL, int RW, ScaleKind SK, YKind YK, bool XOR>
+template <int SPL, int RW, int D, ScaleKind SK, YKind YK, bool XOR>
 __global__ __launch_bounds__(256) void k_qgemv_i4_f16(const u32x4* __restrict__ W,
                                                       const void* __restrict__ S,
                                                       const f16* __restrict__ x,
@@ -76,26 +78,23 @@ __global__ __launch_bounds__(256) void k_qgemv_i4_f16(const u32x4* __restrict__ 
 
     u32x4 q[RW][SPL];
     uint32_t sraw[RW][SPL];
+    // Rows past n_out (last wave only) read the last matrix row instead (an L2 hit);
+    // they are computed but never stored.  Straight-line, in-order issue keeps the
+    // waitcnt bookkeeping exact.
+    auto issue = [&](int r) {
+        const size_t row = (size_t)min(row0 + r, n_out - 1);
 #pragma unroll
-    for (int r = 0; r < RW; ++r) {
-        // Straight-line loads (no branch) keep the waitcnt bookkeeping exact.  In the
-        // last wave, rows past n_out read the last matrix row instead (an L2 hit) and
-        // are computed but never stored.
-        {
-            const size_t row = (size_t)min(row0 + r, n_out - 1);
-#pragma unroll
-            for (int j = 0; j < SPL; ++j) {
-                q[r][j] = __builtin_nontemporal_load(W + row * s_row + sl[j]);
-                if constexpr (SK == ScaleKind::F16)  // aligned u32 holding this scale (g_row is even)
-                    sraw[r][j] = reinterpret_cast<const uint32_t*>(S)[(row * g_row + sl[j] / spg) >> 1];
-                else
-                    sraw[r][j] = load_scale_raw<SK>(S, row * g_row + sl[j] / spg);
-            }
+        for (int j = 0; j < SPL; ++j) {
+            q[r][j] = __builtin_nontemporal_load(W + row * s_row + sl[j]);
+            if constexpr (SK == ScaleKind::F16)  // aligned u32 holding this scale (g_row is even)
+                sraw[r][j] = reinterpret_cast<const uint32_t*>(S)[(row * g_row + sl[j] / spg) >> 1];
+            else
+                sraw[r][j] = load_scale_raw<SK>(S, row * g_row + sl[j] / spg);
         }
-        __builtin_amdgcn_sched_barrier(0);  // rows issue in order: row r arrives first
-    }
-
-    __builtin_amdgcn_sched_barrier(0);  // all loads are in flight before any math
+    };
+#pragma unroll
+    for (int r = 0; r < (D < RW ? D : RW); ++r) issue(r);
+    __builtin_amdgcn_sched_barrier(0);
 
     // x pairs in decode order and, per slice, -8 * sum(x) (offset-binary q = n - 8).
     f16x2 xp[SPL][4][4];
@@ -119,9 +118,12 @@ __global__ __launch_bounds__(256) void k_qgemv_i4_f16(const u32x4* __restrict__ 
         xoff[j] = -8.0f * sx;
     }
 
+    // Software pipeline: keep D rows in flight; issue row r + D, then compute row r.
     float res = 0.f;
 #pragma unroll
     for (int r = 0; r < RW; ++r) {
+        if (r + D < RW) issue(r + D);
+        __builtin_amdgcn_sched_barrier(0);
         float acc = 0.f;
 #pragma unroll
         for (int j = 0; j < SPL; ++j) {
@@ -137,6 +139,7 @@ __global__ __launch_bounds__(256) void k_qgemv_i4_f16(const u32x4* __restrict__ 
         }
         acc = wave_sum(acc);
         res = lane == r ? acc : res;
+        __builtin_amdgcn_sched_barrier(0);
     }
     if (lane < nrows) store_y<YK>(y, row0 + lane, res);
 }
@@ -179,18 +182,25 @@ static int device_cus() {
     return cus[dev];
 }
 
-template <int SPL, int RW, ScaleKind SK, YKind YK>
-static void launch_rw(const QArgs& a, hipStream_t s) {
+template <int SPL, int RW, int D, ScaleKind SK, YKind YK>
+static void launch_rwd(const QArgs& a, hipStream_t s) {
     const int waves = (a.n_out + RW - 1) / RW;
     const dim3 grid((waves + 3) / 4), block(256);
     const u32x4* w = reinterpret_cast<const u32x4*>(a.w);
     const f16* x = reinterpret_cast<const f16*>(a.x);
     if (a.xor_mask)
-        hipLaunchKernelGGL((k_qgemv_i4_f16<SPL, RW, SK, YK, true>), grid, block, 0, s, w, a.s, x,
+        hipLaunchKernelGGL((k_qgemv_i4_f16<SPL, RW, D, SK, YK, true>), grid, block, 0, s, w, a.s, x,
                            a.y, a.n_out, a.k, a.group_size / 32, a.xor_mask);
     else
-        hipLaunchKernelGGL((k_qgemv_i4_f16<SPL, RW, SK, YK, false>), grid, block, 0, s, w, a.s, x,
+        hipLaunchKernelGGL((k_qgemv_i4_f16<SPL, RW, D, SK, YK, false>), grid, block, 0, s, w, a.s, x,
                            a.y, a.n_out, a.k, a.group_size / 32, a.xor_mask);
+}
+
+// One row of prefetch (issue row r+1, then compute row r) measured best on MI355X
+// for config 2; deeper prefetch bunches the arrivals and lengthens the tail.
+template <int SPL, int RW, ScaleKind SK, YKind YK>
+static void launch_rw(const QArgs& a, hipStream_t s) {
+    launch_rwd<SPL, RW, 1, SK, YK>(a, s);
 }
 
 // Rows per wave: enough for 8 waves per CU with equal shares (14336 rows on 256

@@ -2,8 +2,6 @@
 namespace luxhip {
 bool qgemm_small_supported(const QArgs&) { return false; }
 hipError_t launch_qgemm_small(const QArgs&, hipStream_t) { return hipErrorInvalidValue; }
-bool qgemm_i4_large_supported(const QArgs&) { return false; }
-hipError_t launch_qgemm_i4_large(const QArgs&, hipStream_t) { return hipErrorInvalidValue; }
 bool w4a8_supported(const QArgs&) { return false; }
 hipError_t launch_w4a8(const QArgs&, hipStream_t) { return hipErrorInvalidValue; }
 }

@@ -137,6 +137,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=10.0)
+    ap.add_argument("--only", choices=["c2", "c4"], default=None,
+                    help="run one config only (profiling); the JSON line needs both")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (--gpus {args.gpus} requested); "
@@ -150,9 +152,15 @@ def main():
     plugin = W.Plugin()
     ctx = plugin.create_context(0)
     log(f"device: {ctx.info().name.decode()}")
+    if args.only == "c4":
+        c4 = bench_c4(torch, W, ctx, args.steps, args.warmup)
+        log(f"  C4 {c4['per_launch_s']*1e6:.1f} us/launch, {c4['tflops']:.1f} TFLOP/s")
+        return
     log("bench: config 2 int4 GEMV")
     c2 = bench_c2(torch, W, ctx, args.steps, args.warmup)
     log(f"  C2 {c2['per_launch_s']*1e6:.2f} us/launch, {c2['gbs']:.1f} GB/s")
+    if args.only == "c2":
+        return
     c4 = None
     try:
         log("bench: config 4 int4 GEMM M=2048")

@@ -135,9 +135,11 @@ hipError_t launch_qgemv_i4(const QArgs& a, hipStream_t s);
 // Weight-only int4/int8 matmul for small m (bandwidth regime), fp16/bf16/f32 X.
 bool qgemm_small_supported(const QArgs& a);
 hipError_t launch_qgemm_small(const QArgs& a, hipStream_t s);
-// int4 grouped GEMM for large m (MFMA regime).
+// int4 grouped GEMM for large m (MFMA regime).  Needs a device workspace of
+// qgemm_i4_large_workspace(a) bytes (X restaged as fp16), 16-byte aligned.
 bool qgemm_i4_large_supported(const QArgs& a);
-hipError_t launch_qgemm_i4_large(const QArgs& a, hipStream_t s);
+size_t qgemm_i4_large_workspace(const QArgs& a);
+hipError_t launch_qgemm_i4_large(const QArgs& a, void* workspace, hipStream_t s);
 // W4A8 integer MFMA.
 bool w4a8_supported(const QArgs& a);
 hipError_t launch_w4a8(const QArgs& a, hipStream_t s);

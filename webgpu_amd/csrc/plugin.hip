@@ -54,7 +54,28 @@ struct HipCtx {
     std::string name;
     std::string force_fail;  // LUX_HIP_FORCE_FAIL test hook: op name that fails
     hipDeviceProp_t props{};
+    void* ws = nullptr;      // device workspace (staged activations), grown on demand
+    size_t ws_size = 0;
 };
+
+// Workspace of at least `bytes` on the context's device.  Growing it waits for the
+// stream (the old block may still be in use) and calls hipMalloc, so the first call
+// of a shape must not happen inside stream capture.
+void* ensure_workspace(HipCtx* c, size_t bytes) {
+    if (bytes <= c->ws_size) return c->ws;
+    (void)hipStreamSynchronize(c->stream);
+    if (c->ws) (void)hipFree(c->ws);
+    c->ws = nullptr;
+    c->ws_size = 0;
+    const size_t sz = (bytes + 0xFFFFF) & ~(size_t)0xFFFFF;  // 1 MiB granules
+    if (hipMalloc(&c->ws, sz) != hipSuccess) {
+        (void)hipGetLastError();
+        c->ws = nullptr;
+        return nullptr;
+    }
+    c->ws_size = sz;
+    return c->ws;
+}
 
 struct HipBuf {
     void* ptr = nullptr;
@@ -146,6 +167,7 @@ void hip_destroy_context(LuxBackendContext* ctx) {
         (void)hipStreamSynchronize(c->own_stream);
         (void)hipStreamDestroy(c->own_stream);
     }
+    if (c->ws) (void)hipFree(c->ws);
     delete c;
 }
 
@@ -496,7 +518,9 @@ LUX_EXPORT LuxBackendError lux_hip_qmatmul(LuxBackendContext* ctx, const LuxHipQ
     } else if (d->weight_bits == 4 && M == 1) {
         he = launch_qgemv_i4(a, c->stream);
     } else if (d->weight_bits == 4 && qgemm_i4_large_supported(a)) {
-        he = launch_qgemm_i4_large(a, c->stream);
+        void* ws = ensure_workspace(c, qgemm_i4_large_workspace(a));
+        if (!ws) return fail(LUX_BACKEND_ERROR_OUT_OF_MEMORY, "qmatmul: workspace allocation failed");
+        he = launch_qgemm_i4_large(a, ws, c->stream);
     } else if (qgemm_small_supported(a)) {
         he = launch_qgemm_small(a, c->stream);
     } else {

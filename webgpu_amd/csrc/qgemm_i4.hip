@@ -21,6 +21,8 @@
 // through double-buffered LDS (2 x 64 KB): while the MFMAs of stage s run, the
 // global loads of stage s+1 are in flight; they are converted (X) or
 // dequantised (W) and written to the other buffer before one barrier per stage.
+#include <algorithm>
+
 #include "common.hpp"
 
 namespace luxhip {
@@ -35,52 +37,34 @@ __device__ __forceinline__ uint32_t pack_h2(f16 a, f16 b) {
     return __builtin_bit_cast(uint32_t, f16x2{a, b});
 }
 
-// bf16 pair (low, high) -> fp16 pair; exact in the fp16 normal range.
-__device__ __forceinline__ uint32_t bf16x2_to_f16x2(uint32_t v) {
-    const float lo = __builtin_bit_cast(float, v << 16);
-    const float hi = __builtin_bit_cast(float, v & 0xFFFF0000u);
-    return pack_h2((f16)lo, (f16)hi);
+// (a & m) | o in one VOP3; the mask comes from an SGPR, the magic from a VGPR.
+__device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t m, uint32_t o) {
+    uint32_t r;
+    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "s"(m), "v"(o));
+    return r;
 }
 
-template <XKind XK>
-__device__ __forceinline__ void load_x_chunk(const void* X, size_t off, u32x4& v) {
-    // 8 consecutive activations: 16 B for fp16/bf16.
-    v = *reinterpret_cast<const u32x4*>(reinterpret_cast<const uint16_t*>(X) + off);
-}
-
-// 8 activations (as loaded) -> 8 fp16 in natural k order.
-template <XKind XK>
-__device__ __forceinline__ u32x4 x_to_f16(const u32x4 v) {
-    if constexpr (XK == XKind::BF16)
-        return u32x4{bf16x2_to_f16x2(v.x), bf16x2_to_f16x2(v.y), bf16x2_to_f16x2(v.z),
-                     bf16x2_to_f16x2(v.w)};
-    else
-        return v;
-}
-
-// One u32 of 8 offset-binary nibbles (k .. k+7) times scale s -> 8 fp16 (RNE) in
-// natural k order.  (1024 + n) - 1032 is exact in fp16; v_pk_mul_f16 rounds the
-// exact product q*s to nearest-even.
-__device__ __forceinline__ u32x4 dequant8(uint32_t w, f16x2 s2) {
+// One u32 of 8 offset-binary nibbles (k .. k+7) times scale s -> 8 fp16 (RNE) in the
+// staging order (k, k+4, k+1, k+5, k+2, k+6, k+3, k+7).  (1024 + n) - 1032 is exact in
+// fp16; v_pk_mul_f16 rounds the exact product q*s to nearest-even.  15 VALU ops.
+__device__ __forceinline__ u32x4 dequant8(uint32_t w, f16x2 s2, uint32_t magic) {
     const f16x2 OFF = {(f16)1032.0f, (f16)1032.0f};
-    f16x2 p[4];
+    uint32_t o[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        const uint32_t t = ((w >> (4 * i)) & 0x000F000Fu) | 0x64006400u;  // (n_i, n_{i+4})
-        p[i] = (__builtin_bit_cast(f16x2, t) - OFF) * s2;
+        const uint32_t t = and_or(w >> (4 * i), 0x000F000Fu, magic);  // (n_i, n_{i+4})
+        o[i] = __builtin_bit_cast(uint32_t, (__builtin_bit_cast(f16x2, t) - OFF) * s2);
     }
-    // (n0,n4) (n1,n5) (n2,n6) (n3,n7) -> (n0,n1) (n2,n3) (n4,n5) (n6,n7)
-    return u32x4{pack_h2(p[0][0], p[1][0]), pack_h2(p[2][0], p[3][0]), pack_h2(p[0][1], p[1][1]),
-                 pack_h2(p[2][1], p[3][1])};
+    return u32x4{o[0], o[1], o[2], o[3]};
 }
 
-// Same with an fp32 scale: product in fp32 (exact), then RNE to fp16.
+// Same with an fp32 scale: product in fp32 (exact), then RNE to fp16; staging order.
 __device__ __forceinline__ u32x4 dequant8_f32(uint32_t w, float s) {
     uint32_t o[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        const float a = (float)((int)((w >> (8 * i)) & 0xFu) - 8) * s;
-        const float b = (float)((int)((w >> (8 * i + 4)) & 0xFu) - 8) * s;
+        const float a = (float)((int)((w >> (4 * i)) & 0xFu) - 8) * s;
+        const float b = (float)((int)((w >> (4 * i + 16)) & 0xFu) - 8) * s;
         o[i] = pack_h2((f16)a, (f16)b);
     }
     return u32x4{o[0], o[1], o[2], o[3]};
@@ -88,12 +72,39 @@ __device__ __forceinline__ u32x4 dequant8_f32(uint32_t w, float s) {
 
 }  // namespace
 
-template <XKind XK, ScaleKind SK, YKind YK>
-__global__ __launch_bounds__(NT) void k_qgemm_i4_large(const void* __restrict__ X,
-                                                       const uint32_t* __restrict__ W,
-                                                       const void* __restrict__ S,
-                                                       void* __restrict__ Y, int M, int N, int K,
-                                                       int gs, uint32_t xor_mask) {
+// X -> fp16 in staging order.  Runs once per call ahead of the GEMM, so each
+// activation is converted once instead of once per n tile (56 times on config 4).
+// Groups of 8 along k are reordered (k, k+4, k+1, k+5, ...), the order in which
+// dequant8 emits weights; both MFMA operands then agree element by element.
+template <XKind XK>
+__global__ __launch_bounds__(256) void k_x_to_f16_staged(const void* __restrict__ X,
+                                                         u32x4* __restrict__ out, size_t n8) {
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n8; i += (size_t)gridDim.x * 256) {
+        const u32x4 v = reinterpret_cast<const u32x4*>(X)[i];
+        f16 h[8];
+        if constexpr (XK == XKind::BF16) {
+            const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                h[2 * q] = (f16)__builtin_bit_cast(float, w[q] << 16);
+                h[2 * q + 1] = (f16)__builtin_bit_cast(float, w[q] & 0xFFFF0000u);
+            }
+        } else {
+            const f16x8 f = __builtin_bit_cast(f16x8, v);
+#pragma unroll
+            for (int q = 0; q < 8; ++q) h[q] = f[q];
+        }
+        out[i] = u32x4{pack_h2(h[0], h[4]), pack_h2(h[1], h[5]), pack_h2(h[2], h[6]),
+                       pack_h2(h[3], h[7])};
+    }
+}
+
+// GEMM over the staged X (fp16, staging order) and int4 W.
+template <ScaleKind SK, YKind YK>
+__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 1)))
+void k_qgemm_i4_large(const f16* __restrict__ X, const uint32_t* __restrict__ W,
+                      const void* __restrict__ S, void* __restrict__ Y, int M, int N, int K,
+                      int gs, uint32_t xor_mask) {
     extern __shared__ __attribute__((aligned(16))) f16 lds[];
     f16* xs = lds;                          // [2][BM][LDS_ROW]
     f16* ws = lds + 2 * BM * LDS_ROW;       // [2][BN][LDS_ROW]
@@ -103,59 +114,60 @@ __global__ __launch_bounds__(NT) void k_qgemm_i4_large(const void* __restrict__ 
     const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
     const int G = K / gs;
 
-    // ---- global -> register staging for one stage -------------------------------
+    // Raw buffer loads: one SGPR resource per operand, 32-bit VGPR offsets fixed across
+    // stages, the K position in the scalar offset.  Rows past M / N get an offset past
+    // the resource size, which the hardware reads as zeros.
+    const uint32_t xbytes = (uint32_t)((size_t)M * K * 2), wbytes = (uint32_t)((size_t)N * K / 2);
+    const __amdgpu_buffer_rsrc_t rx =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<f16*>(X), (short)0, (int)xbytes, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rw =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint32_t*>(W), (short)0, (int)wbytes, 0x00020000);
     // X: 256 rows x 64 k = 2048 chunks of 8; thread t takes chunks t + 256 i (i < 8):
     // row = (t >> 3) + 32 i, k-chunk = t & 7 (each row read as 128 contiguous bytes).
     // W: row t of the n tile, 64 k = 8 words (2 x 16 B) + the scales of 2 groups of 32.
-    u32x4 xr[8];
-    u32x4 wr[2];
-    uint32_t sr[2];
     const int xrow = tid >> 3, xk = (tid & 7) * 8;
-    auto load_stage = [&](int k0) {
+    uint32_t xoff[8];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const int m = min(m0 + xrow + 32 * i, M - 1);
-            load_x_chunk<XK>(X, (size_t)m * K + k0 + xk, xr[i]);
-        }
-        const int n = min(n0 + tid, N - 1);
-        const u32x4* wp = reinterpret_cast<const u32x4*>(W + ((size_t)n * K + k0) / 8);
-        wr[0] = __builtin_nontemporal_load(wp);
-        wr[1] = __builtin_nontemporal_load(wp + 1);
-        sr[0] = load_scale_raw<SK>(S, (size_t)n * G + k0 / gs);
-        sr[1] = load_scale_raw<SK>(S, (size_t)n * G + (k0 + 32) / gs);
+    for (int i = 0; i < 8; ++i) {
+        const int m = m0 + xrow + 32 * i;
+        xoff[i] = m < M ? (uint32_t)(((size_t)m * K + xk) * 2) : xbytes;
+    }
+    const uint32_t woff = n0 + tid < N ? (uint32_t)((size_t)(n0 + tid) * (K / 2)) : wbytes;
+    const int srow = min(n0 + tid, N - 1);
+    const uint32_t magic = 0x64006400u;
+
+    u32x4 xr[8], wr[2];
+    uint32_t sr[2];
+    auto load_stage = [&](int k0) {
+        k0 = __builtin_amdgcn_readfirstlane(k0);  // uniform: scalar offset in an SGPR
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            xr[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, (int)xoff[i], k0 * 2, 0));
+        wr[0] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rw, (int)woff, k0 / 2, 0));
+        wr[1] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rw, (int)woff + 16, k0 / 2, 0));
+        sr[0] = load_scale_raw<SK>(S, (size_t)srow * G + k0 / gs);
+        sr[1] = load_scale_raw<SK>(S, (size_t)srow * G + (k0 + 32) / gs);
     };
     auto store_stage = [&](int buf) {
         f16* xb = xs + buf * BM * LDS_ROW;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const int r = xrow + 32 * i;
-            const bool ok = m0 + r < M;
-            u32x4 v = x_to_f16<XK>(xr[i]);
-            if (!ok) v = u32x4{0u, 0u, 0u, 0u};
-            *reinterpret_cast<u32x4*>(xb + r * LDS_ROW + xk) = v;
-        }
+        for (int i = 0; i < 8; ++i)
+            *reinterpret_cast<u32x4*>(xb + (xrow + 32 * i) * LDS_ROW + xk) = xr[i];
         f16* wb = ws + buf * BN * LDS_ROW + tid * LDS_ROW;
-        const bool nok = n0 + tid < N;
-        uint32_t words[8] = {wr[0].x, wr[0].y, wr[0].z, wr[0].w, wr[1].x, wr[1].y, wr[1].z, wr[1].w};
+        const uint32_t words[8] = {wr[0].x, wr[0].y, wr[0].z, wr[0].w, wr[1].x, wr[1].y, wr[1].z, wr[1].w};
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
             if constexpr (SK == ScaleKind::F16) {
-                const f16 s = __builtin_bit_cast(f16, (uint16_t)sr[h]);
-                const f16x2 s2 = {s, s};
+                const f16 sc = __builtin_bit_cast(f16, (uint16_t)sr[h]);
+                const f16x2 s2 = {sc, sc};
 #pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    u32x4 v = dequant8(words[4 * h + q] ^ xor_mask, s2);
-                    if (!nok) v = u32x4{0u, 0u, 0u, 0u};
-                    *reinterpret_cast<u32x4*>(wb + 32 * h + 8 * q) = v;
-                }
+                for (int q = 0; q < 4; ++q)
+                    *reinterpret_cast<u32x4*>(wb + 32 * h + 8 * q) = dequant8(words[4 * h + q] ^ xor_mask, s2, magic);
             } else {
-                const float s = scale_from_raw<SK>(sr[h]);
+                const float sc = scale_from_raw<SK>(sr[h]);
 #pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    u32x4 v = dequant8_f32(words[4 * h + q] ^ xor_mask, s);
-                    if (!nok) v = u32x4{0u, 0u, 0u, 0u};
-                    *reinterpret_cast<u32x4*>(wb + 32 * h + 8 * q) = v;
-                }
+                for (int q = 0; q < 4; ++q)
+                    *reinterpret_cast<u32x4*>(wb + 32 * h + 8 * q) = dequant8_f32(words[4 * h + q] ^ xor_mask, sc);
             }
         }
     };
@@ -181,24 +193,28 @@ __global__ __launch_bounds__(NT) void k_qgemm_i4_large(const void* __restrict__ 
         if (s + 1 < nstages) load_stage((s + 1) * BK);
         const f16* xb = xs + buf * BM * LDS_ROW;
         const f16* wb = ws + buf * BN * LDS_ROW;
-#pragma unroll
-        for (int kk = 0; kk < BK; kk += 16) {
-            f16x8 a[4], b[4];
+        // Operands double-buffered across the 4 k-steps: the reads for step kk+1 are
+        // issued ahead of the 16 MFMAs of step kk.
+        f16x8 a[2][4], b[2][4];
+        auto read_ops = [&](int kk, f16x8 (&av)[4], f16x8 (&bv)[4]) {
 #pragma unroll
             for (int i = 0; i < 4; ++i)
-                a[i] = *reinterpret_cast<const f16x8*>(xb + (arow + 32 * i) * LDS_ROW + kk + kofs);
+                av[i] = *reinterpret_cast<const f16x8*>(xb + (arow + 32 * i) * LDS_ROW + 16 * kk + kofs);
 #pragma unroll
             for (int j = 0; j < 4; ++j)
-                b[j] = *reinterpret_cast<const f16x8*>(wb + (brow + 32 * j) * LDS_ROW + kk + kofs);
+                bv[j] = *reinterpret_cast<const f16x8*>(wb + (brow + 32 * j) * LDS_ROW + 16 * kk + kofs);
+        };
+        read_ops(0, a[0], b[0]);
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) {
+            if (kk + 1 < 4) read_ops(kk + 1, a[(kk + 1) & 1], b[(kk + 1) & 1]);
 #pragma unroll
             for (int i = 0; i < 4; ++i)
 #pragma unroll
                 for (int j = 0; j < 4; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], b[j], acc[i][j], 0, 0, 0);
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[kk & 1][i], b[kk & 1][j], acc[i][j], 0, 0, 0);
         }
-        if (s + 1 < nstages) {
-            store_stage(buf ^ 1);
-        }
+        if (s + 1 < nstages) store_stage(buf ^ 1);
         __syncthreads();
     }
 
@@ -218,48 +234,57 @@ __global__ __launch_bounds__(NT) void k_qgemm_i4_large(const void* __restrict__ 
 }
 
 bool qgemm_i4_large_supported(const QArgs& a) {
+    // Buffer resources carry 32-bit byte offsets: X (as fp16) and W stay below 2 GiB.
     return a.wbits == 4 && a.m >= 2 && (a.x_kind == XKind::BF16 || a.x_kind == XKind::F16) &&
            a.k % BK == 0 && a.group_size % 32 == 0 && a.scale_kind != ScaleKind::None &&
-           a.y_kind != YKind::I32 && ((uintptr_t)a.x & 15u) == 0 && ((uintptr_t)a.w & 15u) == 0;
+           a.y_kind != YKind::I32 && (size_t)a.m * a.k * 2 < (1ull << 31) &&
+           (size_t)a.n_out * a.k / 2 < (1ull << 31) && ((uintptr_t)a.x & 15u) == 0 &&
+           ((uintptr_t)a.w & 15u) == 0;
 }
 
-template <XKind XK, ScaleKind SK, YKind YK>
-static void launch_t(const QArgs& a, hipStream_t s) {
+template <ScaleKind SK, YKind YK>
+static void launch_t(const QArgs& a, const f16* xst, hipStream_t s) {
     const dim3 grid((a.n_out + BN - 1) / BN, (a.m + BM - 1) / BM), block(NT);
     const size_t lds = (size_t)2 * (BM + BN) * LDS_ROW * sizeof(f16);
     static bool attr = [] {
-        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&k_qgemm_i4_large<XK, SK, YK>),
+        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&k_qgemm_i4_large<SK, YK>),
                                   hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
         return true;
     }();
     (void)attr;
-    hipLaunchKernelGGL((k_qgemm_i4_large<XK, SK, YK>), grid, block, lds, s, a.x,
+    hipLaunchKernelGGL((k_qgemm_i4_large<SK, YK>), grid, block, lds, s, xst,
                        reinterpret_cast<const uint32_t*>(a.w), a.s, a.y, a.m, a.n_out, a.k,
                        a.group_size, a.xor_mask);
 }
 
-template <XKind XK, ScaleKind SK>
-static bool launch_y(const QArgs& a, hipStream_t s) {
+template <ScaleKind SK>
+static bool launch_y(const QArgs& a, const f16* xst, hipStream_t s) {
     switch (a.y_kind) {
-        case YKind::F32: launch_t<XK, SK, YKind::F32>(a, s); return true;
-        case YKind::F16: launch_t<XK, SK, YKind::F16>(a, s); return true;
-        case YKind::BF16: launch_t<XK, SK, YKind::BF16>(a, s); return true;
+        case YKind::F32: launch_t<SK, YKind::F32>(a, xst, s); return true;
+        case YKind::F16: launch_t<SK, YKind::F16>(a, xst, s); return true;
+        case YKind::BF16: launch_t<SK, YKind::BF16>(a, xst, s); return true;
         default: return false;
     }
 }
 
-template <XKind XK>
-static bool launch_s(const QArgs& a, hipStream_t s) {
+size_t qgemm_i4_large_workspace(const QArgs& a) { return (size_t)a.m * a.k * sizeof(f16); }
+
+hipError_t launch_qgemm_i4_large(const QArgs& a, void* workspace, hipStream_t s) {
+    const size_t n8 = (size_t)a.m * a.k / 8;
+    const unsigned blocks = (unsigned)std::min<size_t>((n8 + 255) / 256, 4096);
+    u32x4* xst = reinterpret_cast<u32x4*>(workspace);
+    if (a.x_kind == XKind::BF16)
+        hipLaunchKernelGGL(k_x_to_f16_staged<XKind::BF16>, dim3(blocks), dim3(256), 0, s, a.x, xst, n8);
+    else
+        hipLaunchKernelGGL(k_x_to_f16_staged<XKind::F16>, dim3(blocks), dim3(256), 0, s, a.x, xst, n8);
+    const f16* xh = reinterpret_cast<const f16*>(workspace);
+    bool ok = false;
     switch (a.scale_kind) {
-        case ScaleKind::F16: return launch_y<XK, ScaleKind::F16>(a, s);
-        case ScaleKind::F32: return launch_y<XK, ScaleKind::F32>(a, s);
-        case ScaleKind::GroupScale: return launch_y<XK, ScaleKind::GroupScale>(a, s);
-        default: return false;
+        case ScaleKind::F16: ok = launch_y<ScaleKind::F16>(a, xh, s); break;
+        case ScaleKind::F32: ok = launch_y<ScaleKind::F32>(a, xh, s); break;
+        case ScaleKind::GroupScale: ok = launch_y<ScaleKind::GroupScale>(a, xh, s); break;
+        default: break;
     }
-}
-
-hipError_t launch_qgemm_i4_large(const QArgs& a, hipStream_t s) {
-    bool ok = a.x_kind == XKind::BF16 ? launch_s<XKind::BF16>(a, s) : launch_s<XKind::F16>(a, s);
     if (!ok) return hipErrorInvalidValue;
     return hipGetLastError();
 }

@@ -15,12 +15,14 @@
 // the stated 1e-3 (the bf16 output rounding alone is worth 1.7e-3 against the
 // unrounded oracle).
 //
-// Tiling (gfx950): 256 threads = 4 waves in a 2 x 2 grid; block tile 256 (m) x
-// 256 (n); each wave owns 128 x 128 = 4 x 4 tiles of v_mfma_f32_32x32x16_f16
-// (256 fp32 accumulators per lane, held in AGPRs).  K advances 64 per stage
-// through double-buffered LDS (2 x 64 KB): while the MFMAs of stage s run, the
-// global loads of stage s+1 are in flight; they are converted (X) or
-// dequantised (W) and written to the other buffer before one barrier per stage.
+// Tiling (gfx950): 512 threads = 8 waves in a 2 (m) x 4 (n) grid, two per SIMD so
+// one wave's MFMAs cover the other's loads and dequant; block tile 256 (m) x 256
+// (n); each wave owns 128 x 64 = 4 x 2 tiles of v_mfma_f32_32x32x16_f16 (128 fp32
+// accumulators per lane, in AGPRs).  K advances 64 per stage through
+// double-buffered LDS (2 x 72 KB): while the MFMAs of stage s run, the global loads
+// of stage s+1 are in flight; W is dequantised and both tiles are written to the
+// other buffer before one barrier per stage.  X is restaged to fp16 once per call
+// by a pre-pass.
 #include <algorithm>
 
 #include "common.hpp"
@@ -31,7 +33,7 @@ namespace {
 
 constexpr int BM = 256, BN = 256, BK = 64;
 constexpr int LDS_ROW = BK + 8;  // halves per LDS row: 144 B stride keeps b128 reads conflict-free
-constexpr int NT = 256;
+constexpr int NT = 512;  // 8 waves: 2 (m) x 4 (n), two per SIMD
 
 __device__ __forceinline__ uint32_t pack_h2(f16 a, f16 b) {
     return __builtin_bit_cast(uint32_t, f16x2{a, b});
@@ -101,7 +103,7 @@ __global__ __launch_bounds__(256) void k_x_to_f16_staged(const void* __restrict_
 
 // GEMM over the staged X (fp16, staging order) and int4 W.
 template <ScaleKind SK, YKind YK>
-__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 1)))
+__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void k_qgemm_i4_large(const f16* __restrict__ X, const uint32_t* __restrict__ W,
                       const void* __restrict__ S, void* __restrict__ Y, int M, int N, int K,
                       int gs, uint32_t xor_mask) {
@@ -110,7 +112,7 @@ void k_qgemm_i4_large(const f16* __restrict__ X, const uint32_t* __restrict__ W,
     f16* ws = lds + 2 * BM * LDS_ROW;       // [2][BN][LDS_ROW]
 
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-    const int wm = wv >> 1, wn = wv & 1;    // 2 x 2 waves
+    const int wm = wv >> 2, wn = wv & 3;    // wave tile: 128 (m) x 64 (n)
     const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
     const int G = K / gs;
 
@@ -122,61 +124,58 @@ void k_qgemm_i4_large(const f16* __restrict__ X, const uint32_t* __restrict__ W,
         __builtin_amdgcn_make_buffer_rsrc(const_cast<f16*>(X), (short)0, (int)xbytes, 0x00020000);
     const __amdgpu_buffer_rsrc_t rw =
         __builtin_amdgcn_make_buffer_rsrc(const_cast<uint32_t*>(W), (short)0, (int)wbytes, 0x00020000);
-    // X: 256 rows x 64 k = 2048 chunks of 8; thread t takes chunks t + 256 i (i < 8):
-    // row = (t >> 3) + 32 i, k-chunk = t & 7 (each row read as 128 contiguous bytes).
-    // W: row t of the n tile, 64 k = 8 words (2 x 16 B) + the scales of 2 groups of 32.
+    // X: 256 rows x 64 k = 2048 chunks of 8; thread t takes chunks t + 512 i (i < 4):
+    // row = (t >> 3) + 64 i, k-chunk = t & 7 (each row read as 128 contiguous bytes).
+    // W: 2 threads per row of the n tile; thread t takes row t / 2, k half t % 2
+    // (32 nibbles = 16 B, one scale group of 32).
     const int xrow = tid >> 3, xk = (tid & 7) * 8;
-    uint32_t xoff[8];
+    uint32_t xoff[4];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        const int m = m0 + xrow + 32 * i;
+    for (int i = 0; i < 4; ++i) {
+        const int m = m0 + xrow + 64 * i;
         xoff[i] = m < M ? (uint32_t)(((size_t)m * K + xk) * 2) : xbytes;
     }
-    const uint32_t woff = n0 + tid < N ? (uint32_t)((size_t)(n0 + tid) * (K / 2)) : wbytes;
-    const int srow = min(n0 + tid, N - 1);
+    const int wr_row = tid >> 1, wh = tid & 1;
+    const uint32_t woff = n0 + wr_row < N ? (uint32_t)((size_t)(n0 + wr_row) * (K / 2) + 16 * wh) : wbytes;
+    const int srow = min(n0 + wr_row, N - 1);
     const uint32_t magic = 0x64006400u;
 
-    u32x4 xr[8], wr[2];
-    uint32_t sr[2];
+    u32x4 xr[4], wr;
+    uint32_t sr;
     auto load_stage = [&](int k0) {
         k0 = __builtin_amdgcn_readfirstlane(k0);  // uniform: scalar offset in an SGPR
 #pragma unroll
-        for (int i = 0; i < 8; ++i)
+        for (int i = 0; i < 4; ++i)
             xr[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, (int)xoff[i], k0 * 2, 0));
-        wr[0] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rw, (int)woff, k0 / 2, 0));
-        wr[1] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rw, (int)woff + 16, k0 / 2, 0));
-        sr[0] = load_scale_raw<SK>(S, (size_t)srow * G + k0 / gs);
-        sr[1] = load_scale_raw<SK>(S, (size_t)srow * G + (k0 + 32) / gs);
+        wr = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rw, (int)woff, k0 / 2, 0));
+        sr = load_scale_raw<SK>(S, (size_t)srow * G + (k0 + 32 * wh) / gs);
     };
     auto store_stage = [&](int buf) {
         f16* xb = xs + buf * BM * LDS_ROW;
 #pragma unroll
-        for (int i = 0; i < 8; ++i)
-            *reinterpret_cast<u32x4*>(xb + (xrow + 32 * i) * LDS_ROW + xk) = xr[i];
-        f16* wb = ws + buf * BN * LDS_ROW + tid * LDS_ROW;
-        const uint32_t words[8] = {wr[0].x, wr[0].y, wr[0].z, wr[0].w, wr[1].x, wr[1].y, wr[1].z, wr[1].w};
+        for (int i = 0; i < 4; ++i)
+            *reinterpret_cast<u32x4*>(xb + (xrow + 64 * i) * LDS_ROW + xk) = xr[i];
+        f16* wb = ws + buf * BN * LDS_ROW + wr_row * LDS_ROW + 32 * wh;
+        const uint32_t words[4] = {wr.x, wr.y, wr.z, wr.w};
+        if constexpr (SK == ScaleKind::F16) {
+            const f16 sc = __builtin_bit_cast(f16, (uint16_t)sr);
+            const f16x2 s2 = {sc, sc};
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            if constexpr (SK == ScaleKind::F16) {
-                const f16 sc = __builtin_bit_cast(f16, (uint16_t)sr[h]);
-                const f16x2 s2 = {sc, sc};
+            for (int q = 0; q < 4; ++q)
+                *reinterpret_cast<u32x4*>(wb + 8 * q) = dequant8(words[q] ^ xor_mask, s2, magic);
+        } else {
+            const float sc = scale_from_raw<SK>(sr);
 #pragma unroll
-                for (int q = 0; q < 4; ++q)
-                    *reinterpret_cast<u32x4*>(wb + 32 * h + 8 * q) = dequant8(words[4 * h + q] ^ xor_mask, s2, magic);
-            } else {
-                const float sc = scale_from_raw<SK>(sr[h]);
-#pragma unroll
-                for (int q = 0; q < 4; ++q)
-                    *reinterpret_cast<u32x4*>(wb + 32 * h + 8 * q) = dequant8_f32(words[4 * h + q] ^ xor_mask, sc);
-            }
+            for (int q = 0; q < 4; ++q)
+                *reinterpret_cast<u32x4*>(wb + 8 * q) = dequant8_f32(words[q] ^ xor_mask, sc);
         }
     };
 
-    f32x16 acc[4][4];
+    f32x16 acc[4][2];
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = f32x16{};
+        for (int j = 0; j < 2; ++j) acc[i][j] = f32x16{};
 
     const int nstages = K / BK;
     load_stage(0);
@@ -185,7 +184,7 @@ void k_qgemm_i4_large(const f16* __restrict__ X, const uint32_t* __restrict__ W,
 
     // MFMA operand addressing (v_mfma_f32_32x32x16_f16): A row = lane % 32, B column =
     // lane % 32, both taking k = 8 * (lane / 32) + 0..7 of the 16-k step.
-    const int arow = wm * 128 + (lane & 31), brow = wn * 128 + (lane & 31);
+    const int arow = wm * 128 + (lane & 31), brow = wn * 64 + (lane & 31);
     const int kofs = (lane >> 5) * 8;
 
     for (int s = 0; s < nstages; ++s) {
@@ -194,14 +193,14 @@ void k_qgemm_i4_large(const f16* __restrict__ X, const uint32_t* __restrict__ W,
         const f16* xb = xs + buf * BM * LDS_ROW;
         const f16* wb = ws + buf * BN * LDS_ROW;
         // Operands double-buffered across the 4 k-steps: the reads for step kk+1 are
-        // issued ahead of the 16 MFMAs of step kk.
-        f16x8 a[2][4], b[2][4];
-        auto read_ops = [&](int kk, f16x8 (&av)[4], f16x8 (&bv)[4]) {
+        // issued ahead of the 8 MFMAs of step kk.
+        f16x8 a[2][4], b[2][2];
+        auto read_ops = [&](int kk, f16x8 (&av)[4], f16x8 (&bv)[2]) {
 #pragma unroll
             for (int i = 0; i < 4; ++i)
                 av[i] = *reinterpret_cast<const f16x8*>(xb + (arow + 32 * i) * LDS_ROW + 16 * kk + kofs);
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
+            for (int j = 0; j < 2; ++j)
                 bv[j] = *reinterpret_cast<const f16x8*>(wb + (brow + 32 * j) * LDS_ROW + 16 * kk + kofs);
         };
         read_ops(0, a[0], b[0]);
@@ -211,7 +210,7 @@ void k_qgemm_i4_large(const f16* __restrict__ X, const uint32_t* __restrict__ W,
 #pragma unroll
             for (int i = 0; i < 4; ++i)
 #pragma unroll
-                for (int j = 0; j < 4; ++j)
+                for (int j = 0; j < 2; ++j)
                     acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[kk & 1][i], b[kk & 1][j], acc[i][j], 0, 0, 0);
         }
         if (s + 1 < nstages) store_stage(buf ^ 1);
@@ -223,8 +222,8 @@ void k_qgemm_i4_large(const f16* __restrict__ X, const uint32_t* __restrict__ W,
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int n = n0 + wn * 128 + 32 * j + (lane & 31);
+        for (int j = 0; j < 2; ++j) {
+            const int n = n0 + wn * 64 + 32 * j + (lane & 31);
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int m = m0 + wm * 128 + 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);

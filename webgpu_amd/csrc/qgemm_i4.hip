@@ -140,31 +140,39 @@ void k_qgemm_i4_large(const f16* __restrict__ X, const uint32_t* __restrict__ W,
     const int srow = min(n0 + wr_row, N - 1);
     const uint32_t magic = 0x64006400u;
 
-    u32x4 xr[4], wr;
-    uint32_t sr;
-    auto load_stage = [&](int k0) {
-        k0 = __builtin_amdgcn_readfirstlane(k0);  // uniform: scalar offset in an SGPR
+    // Staging registers.  X (an L2/MALL hit: every n tile reads it) is loaded one stage
+    // ahead; W (the HBM stream) two stages ahead, in two register sets.
+    u32x4 xr[4];
+    struct WRegs {
+        u32x4 wr;
+        uint32_t sr;
+    };
+    auto load_x = [&](int k0) {
+        k0 = __builtin_amdgcn_readfirstlane(min(k0, K - BK));  // uniform; clamped in range
 #pragma unroll
         for (int i = 0; i < 4; ++i)
             xr[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, (int)xoff[i], k0 * 2, 0));
-        wr = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rw, (int)woff, k0 / 2, 0));
-        sr = load_scale_raw<SK>(S, (size_t)srow * G + (k0 + 32 * wh) / gs);
     };
-    auto store_stage = [&](int buf) {
+    auto load_w = [&](WRegs& R, int k0) {
+        k0 = __builtin_amdgcn_readfirstlane(min(k0, K - BK));
+        R.wr = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rw, (int)woff, k0 / 2, 0));
+        R.sr = load_scale_raw<SK>(S, (size_t)srow * G + (k0 + 32 * wh) / gs);
+    };
+    auto store_stage = [&](const WRegs& R, int buf) {
         f16* xb = xs + buf * BM * LDS_ROW;
 #pragma unroll
         for (int i = 0; i < 4; ++i)
             *reinterpret_cast<u32x4*>(xb + (xrow + 64 * i) * LDS_ROW + xk) = xr[i];
         f16* wb = ws + buf * BN * LDS_ROW + wr_row * LDS_ROW + 32 * wh;
-        const uint32_t words[4] = {wr.x, wr.y, wr.z, wr.w};
+        const uint32_t words[4] = {R.wr.x, R.wr.y, R.wr.z, R.wr.w};
         if constexpr (SK == ScaleKind::F16) {
-            const f16 sc = __builtin_bit_cast(f16, (uint16_t)sr);
+            const f16 sc = __builtin_bit_cast(f16, (uint16_t)R.sr);
             const f16x2 s2 = {sc, sc};
 #pragma unroll
             for (int q = 0; q < 4; ++q)
                 *reinterpret_cast<u32x4*>(wb + 8 * q) = dequant8(words[q] ^ xor_mask, s2, magic);
         } else {
-            const float sc = scale_from_raw<SK>(sr);
+            const float sc = scale_from_raw<SK>(R.sr);
 #pragma unroll
             for (int q = 0; q < 4; ++q)
                 *reinterpret_cast<u32x4*>(wb + 8 * q) = dequant8_f32(words[q] ^ xor_mask, sc);
@@ -177,23 +185,16 @@ void k_qgemm_i4_large(const f16* __restrict__ X, const uint32_t* __restrict__ W,
 #pragma unroll
         for (int j = 0; j < 2; ++j) acc[i][j] = f32x16{};
 
-    const int nstages = K / BK;
-    load_stage(0);
-    store_stage(0);
-    __syncthreads();
-
     // MFMA operand addressing (v_mfma_f32_32x32x16_f16): A row = lane % 32, B column =
     // lane % 32, both taking k = 8 * (lane / 32) + 0..7 of the 16-k step.
     const int arow = wm * 128 + (lane & 31), brow = wn * 64 + (lane & 31);
     const int kofs = (lane >> 5) * 8;
 
-    for (int s = 0; s < nstages; ++s) {
-        const int buf = s & 1;
-        if (s + 1 < nstages) load_stage((s + 1) * BK);
+    // 4 k-steps of 8 MFMAs from LDS buffer `buf`; operands double-buffered across
+    // the k-steps (reads for step kk+1 go out ahead of the MFMAs of step kk).
+    auto compute = [&](int buf) {
         const f16* xb = xs + buf * BM * LDS_ROW;
         const f16* wb = ws + buf * BN * LDS_ROW;
-        // Operands double-buffered across the 4 k-steps: the reads for step kk+1 are
-        // issued ahead of the 8 MFMAs of step kk.
         f16x8 a[2][4], b[2][2];
         auto read_ops = [&](int kk, f16x8 (&av)[4], f16x8 (&bv)[2]) {
 #pragma unroll
@@ -213,9 +214,33 @@ void k_qgemm_i4_large(const f16* __restrict__ X, const uint32_t* __restrict__ W,
                 for (int j = 0; j < 2; ++j)
                     acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[kk & 1][i], b[kk & 1][j], acc[i][j], 0, 0, 0);
         }
-        if (s + 1 < nstages) store_stage(buf ^ 1);
+    };
+
+    // Stages past the end load a clamped (valid) stage into a buffer nobody reads.
+    const int nstages = K / BK;
+    WRegs R0, R1;
+    load_x(0);
+    load_w(R0, 0);
+    load_w(R1, BK);
+    store_stage(R0, 0);
+    __syncthreads();
+    // Two stages per iteration (static register sets); an odd stage count ends with
+    // one more stage from buffer 0.
+    const int npairs = nstages >> 1;
+    for (int p = 0; p < npairs; ++p) {
+        const int s = 2 * p;
+        load_x((s + 1) * BK);
+        load_w(R0, (s + 2) * BK);
+        compute(0);
+        store_stage(R1, 1);
+        __syncthreads();
+        load_x((s + 2) * BK);
+        load_w(R1, (s + 3) * BK);
+        compute(1);
+        store_stage(R0, 0);
         __syncthreads();
     }
+    if (nstages & 1) compute(0);
 
     // Epilogue: D[i][j] of a 32x32 tile sits in lane j + 32 * ((i / 4) & 1), register
     // 4 * (i / 8) + i % 4.

@@ -140,29 +140,25 @@ void k_qgemm_i4_large(const f16* __restrict__ X, const uint32_t* __restrict__ W,
     const int srow = min(n0 + wr_row, N - 1);
     const uint32_t magic = 0x64006400u;
 
-    // Staging registers.  X (an L2/MALL hit: every n tile reads it) is loaded one stage
-    // ahead; W (the HBM stream) two stages ahead, in two register sets.
-    u32x4 xr[4];
-    struct WRegs {
-        u32x4 wr;
+    // Staging registers, two sets: the data of stage t is loaded during stage t-2 and
+    // written to LDS early in stage t-1, interleaved with that stage's MFMAs.
+    struct Regs {
+        u32x4 xr[4], wr;
         uint32_t sr;
     };
-    auto load_x = [&](int k0) {
+    auto load_stage = [&](Regs& R, int k0) {
         k0 = __builtin_amdgcn_readfirstlane(min(k0, K - BK));  // uniform; clamped in range
 #pragma unroll
         for (int i = 0; i < 4; ++i)
-            xr[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, (int)xoff[i], k0 * 2, 0));
-    };
-    auto load_w = [&](WRegs& R, int k0) {
-        k0 = __builtin_amdgcn_readfirstlane(min(k0, K - BK));
+            R.xr[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, (int)xoff[i], k0 * 2, 0));
         R.wr = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rw, (int)woff, k0 / 2, 0));
         R.sr = load_scale_raw<SK>(S, (size_t)srow * G + (k0 + 32 * wh) / gs);
     };
-    auto store_stage = [&](const WRegs& R, int buf) {
+    auto store_stage = [&](const Regs& R, int buf) {
         f16* xb = xs + buf * BM * LDS_ROW;
 #pragma unroll
         for (int i = 0; i < 4; ++i)
-            *reinterpret_cast<u32x4*>(xb + (xrow + 64 * i) * LDS_ROW + xk) = xr[i];
+            *reinterpret_cast<u32x4*>(xb + (xrow + 64 * i) * LDS_ROW + xk) = R.xr[i];
         f16* wb = ws + buf * BN * LDS_ROW + wr_row * LDS_ROW + 32 * wh;
         const uint32_t words[4] = {R.wr.x, R.wr.y, R.wr.z, R.wr.w};
         if constexpr (SK == ScaleKind::F16) {
@@ -192,7 +188,11 @@ void k_qgemm_i4_large(const f16* __restrict__ X, const uint32_t* __restrict__ W,
 
     // 4 k-steps of 8 MFMAs from LDS buffer `buf`; operands double-buffered across
     // the k-steps (reads for step kk+1 go out ahead of the MFMAs of step kk).
-    auto compute = [&](int buf) {
+    // One stage: 4 k-steps of 8 MFMAs from LDS buffer `buf`.  Operands are
+    // double-buffered across the k-steps.  After the first k-step the next stage's
+    // registers are dequantised into the other buffer, so that VALU work issues
+    // while this wave's (and the sibling wave's) MFMAs occupy the matrix pipe.
+    auto compute = [&](int buf, const Regs& nxt) {
         const f16* xb = xs + buf * BM * LDS_ROW;
         const f16* wb = ws + buf * BN * LDS_ROW;
         f16x8 a[2][4], b[2][2];
@@ -213,15 +213,15 @@ void k_qgemm_i4_large(const f16* __restrict__ X, const uint32_t* __restrict__ W,
 #pragma unroll
                 for (int j = 0; j < 2; ++j)
                     acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[kk & 1][i], b[kk & 1][j], acc[i][j], 0, 0, 0);
+            if (kk == 0) store_stage(nxt, buf ^ 1);
         }
     };
 
     // Stages past the end load a clamped (valid) stage into a buffer nobody reads.
     const int nstages = K / BK;
-    WRegs R0, R1;
-    load_x(0);
-    load_w(R0, 0);
-    load_w(R1, BK);
+    Regs R0, R1;
+    load_stage(R0, 0);
+    load_stage(R1, BK);
     store_stage(R0, 0);
     __syncthreads();
     // Two stages per iteration (static register sets); an odd stage count ends with
@@ -229,18 +229,14 @@ void k_qgemm_i4_large(const f16* __restrict__ X, const uint32_t* __restrict__ W,
     const int npairs = nstages >> 1;
     for (int p = 0; p < npairs; ++p) {
         const int s = 2 * p;
-        load_x((s + 1) * BK);
-        load_w(R0, (s + 2) * BK);
-        compute(0);
-        store_stage(R1, 1);
+        load_stage(R0, (s + 2) * BK);
+        compute(0, R1);            // stores stage s+1 into buffer 1
         __syncthreads();
-        load_x((s + 2) * BK);
-        load_w(R1, (s + 3) * BK);
-        compute(1);
-        store_stage(R0, 0);
+        load_stage(R1, (s + 3) * BK);
+        compute(1, R0);            // stores stage s+2 into buffer 0
         __syncthreads();
     }
-    if (nstages & 1) compute(0);
+    if (nstages & 1) compute(0, R1);
 
     // Epilogue: D[i][j] of a 32x32 tile sits in lane j + 32 * ((i / 4) & 1), register
     // 4 * (i / 8) + i % 4.

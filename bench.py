@@ -33,6 +33,9 @@ C2 = dict(n_out=14336, k=4096, gs=32)
 C2_BYTES = 14336 * 4096 // 2 + 14336 * (4096 // 32) * 2 + 4096 * 2 + 14336 * 2  # 33,067,008
 C4 = dict(n_out=14336, k=4096, m=2048, gs=32)
 C4_FLOPS = 2 * 2048 * 14336 * 4096
+C3 = dict(n_out=28672, k=8192)
+C5 = dict(n_out=11008, k=4096, m=256, gs=128)
+INT8_MFMA_PEAK_TOPS = 5000.0
 
 
 def log(msg):
@@ -112,6 +115,58 @@ def bench_c4(torch, W, ctx, steps, warmup):
     return {"per_launch_s": per, "tflops": tf, "frac": tf / MFMA_F16_PEAK_TFLOPS, "steps": n}
 
 
+def c3_bytes(m):
+    """Algorithmic HBM bytes of one config-3 call: int8 W + fp16 row scales + X + Y."""
+    return C3["n_out"] * C3["k"] + C3["n_out"] * 2 + m * C3["k"] * 2 + m * C3["n_out"] * 2
+
+
+def bench_c3(torch, W, ctx, m, steps, warmup):
+    from util import int8_weights
+    r = np.random.default_rng(30 + m)
+    q, s = int8_weights(r, C3["n_out"], C3["k"])
+    X = r.standard_normal((m, C3["k"])).astype(np.float16)
+    copies = max(2, -(-512 * 2**20 // q.nbytes))
+    wbs = [ctx.upload(q) for _ in range(copies)]
+    sb, xb = ctx.upload(s), ctx.upload(X)
+    yb = ctx.alloc(m * C3["n_out"] * 2)
+    d = W.qdesc(C3["n_out"], C3["k"], m, 8, C3["k"], 0, W.SCALE_F16, W.F16, W.F16)
+
+    def launch(i):
+        ctx.qmatmul(d, wbs[i % copies], sb, xb, None, yb)
+
+    n = max(3, min(steps, 100))
+    per = timed_graph(torch, ctx, launch, n, max(1, warmup // 4)) / n
+    for b in wbs:
+        b.free()
+    gbs = c3_bytes(m) / per / 1e9
+    return {"m": m, "us_per_launch": round(per * 1e6, 2), "value": round(gbs, 2), "unit": "GB/s",
+            "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS,
+                         "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None}}
+
+
+def bench_c5(torch, W, ctx, steps, warmup):
+    from util import int4_weights, quantize_rows_int8
+    r = np.random.default_rng(5)
+    _, Wp, s = int4_weights(r, C5["n_out"], C5["k"], C5["gs"], 1)
+    a8, asc = quantize_rows_int8(r.standard_normal((C5["m"], C5["k"])).astype(np.float32))
+    wb, sb, xb, asb = ctx.upload(Wp), ctx.upload(s), ctx.upload(a8), ctx.upload(asc)
+    yb = ctx.alloc(C5["m"] * C5["n_out"] * 2)
+    d = W.qdesc(C5["n_out"], C5["k"], C5["m"], 4, C5["gs"], 1, W.SCALE_F16, W.I8, W.F16)
+
+    def launch(i):
+        ctx.qmatmul(d, wb, sb, xb, asb, yb)
+
+    n = max(3, min(steps, 100))
+    per = timed_graph(torch, ctx, launch, n, max(1, warmup // 4)) / n
+    ops = 2 * C5["m"] * C5["n_out"] * C5["k"]
+    nbytes = Wp.nbytes + s.nbytes + a8.nbytes + asc.nbytes + C5["m"] * C5["n_out"] * 2
+    tops = ops / per / 1e12
+    return {"us_per_launch": round(per * 1e6, 2), "value": round(tops, 2), "unit": "TOP/s",
+            "hbm_gbs": round(nbytes / per / 1e9, 2),
+            "roofline": {"bound": "mfma", "achieved": round(tops, 2), "peak": INT8_MFMA_PEAK_TOPS,
+                         "unit": "TOP/s", "frac": round(tops / INT8_MFMA_PEAK_TOPS, 4), "traffic": None}}
+
+
 def cpu_baseline_c2(Wp, s, x, budget_s=10.0):
     import oracle
     sf = s.astype(np.float32).reshape(-1)
@@ -137,7 +192,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=10.0)
-    ap.add_argument("--only", choices=["c2", "c4"], default=None,
+    ap.add_argument("--only", choices=["c2", "c3", "c4", "c5"], default=None,
                     help="run one config only (profiling); the JSON line needs both")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -156,6 +211,15 @@ def main():
         c4 = bench_c4(torch, W, ctx, args.steps, args.warmup)
         log(f"  C4 {c4['per_launch_s']*1e6:.1f} us/launch, {c4['tflops']:.1f} TFLOP/s")
         return
+    if args.only == "c3":
+        for m in (8, 32):
+            c3 = bench_c3(torch, W, ctx, m, args.steps, args.warmup)
+            log(f"  C3 m={m} {c3['us_per_launch']} us/launch, {c3['value']} GB/s")
+        return
+    if args.only == "c5":
+        c5 = bench_c5(torch, W, ctx, args.steps, args.warmup)
+        log(f"  C5 {c5['us_per_launch']} us/launch, {c5['value']} TOP/s, {c5['hbm_gbs']} GB/s")
+        return
     log("bench: config 2 int4 GEMV")
     c2 = bench_c2(torch, W, ctx, args.steps, args.warmup)
     log(f"  C2 {c2['per_launch_s']*1e6:.2f} us/launch, {c2['gbs']:.1f} GB/s")
@@ -168,6 +232,17 @@ def main():
         log(f"  C4 {c4['per_launch_s']*1e6:.1f} us/launch, {c4['tflops']:.1f} TFLOP/s")
     except W.LuxError as e:
         log(f"  C4 skipped: {e}")
+    c3s, c5 = [], None
+    try:
+        log("bench: config 3 int8 GEMM M=8,32")
+        for m in (8, 32):
+            c3s.append(bench_c3(torch, W, ctx, m, args.steps, args.warmup))
+            log(f"  C3 m={m} {c3s[-1]['us_per_launch']} us/launch, {c3s[-1]['value']} GB/s")
+        log("bench: config 5 W4A8 M=256")
+        c5 = bench_c5(torch, W, ctx, args.steps, args.warmup)
+        log(f"  C5 {c5['us_per_launch']} us/launch, {c5['value']} TOP/s")
+    except W.LuxError as e:
+        log(f"  C3/C5 skipped: {e}")
     cpu = None
     if not args.no_cpu_baseline:
         log("bench: CPU baseline (oracle)")
@@ -201,6 +276,8 @@ def main():
             "roofline": {"bound": "mfma", "achieved": round(c4["tflops"], 2),
                          "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s",
                          "frac": round(c4["frac"], 4), "traffic": None}},
+        "int8_gemm_c3": c3s or None,
+        "w4a8_gemm_c5": c5,
     }
     print(json.dumps(out), flush=True)
     ctx.close()

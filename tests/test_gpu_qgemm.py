@@ -103,3 +103,56 @@ def test_int4_gemm_exact_grid(ctx):
     got = _run(ctx, d, Wp, s, X, n_out, m, "f32")
     ref = oracle.matmul_nax_grouped_tokens(Wp, s.astype(np.float32).reshape(-1), Xf, gs)
     assert np.array_equal(got, ref.astype(np.float64))
+
+
+# --------------------------------------------------------------------------- small m
+@pytest.mark.parametrize("m", [8, 32])
+def test_config3_int8_per_row(ctx, m):
+    """C3: W 28672 x 8192 int8 U[-127,127], per-row fp16 scales U(0.001,0.01),
+    X m x 8192 fp16 N(0,1), fp16 out; oracle = dequantize_nax_int8_group (gs = K)
+    followed by the sequential-k matmul."""
+    r = rng(30 + m)
+    n_out, K = 28672, 8192
+    q, s = int8_weights(r, n_out, K)
+    X = r.standard_normal((m, K)).astype(np.float16)
+    d = W.qdesc(n_out, K, m, 8, K, 0, W.SCALE_F16, W.F16, W.F16)
+    got = _run(ctx, d, q, s, X, n_out, m, "f16")
+    ref = oracle.matmul_int8_dequant_tokens(q, s.astype(np.float32).reshape(-1),
+                                            X.astype(np.float32), K)
+    st = compare(got, round_to(ref, "f16"), f"C3 m={m}")
+    print(f"C3 m={m} rel-L2 {st['rel_l2']:.3e}")
+
+
+@pytest.mark.parametrize("n_out,K,m,gs,xd,y", [
+    (100, 256, 1, 256, "f16", "f32"),
+    (1000, 512, 5, 512, "bf16", "bf16"),
+    (513, 1024, 64, 128, "f16", "f32"),
+    (256, 768, 70, 768, "f32", "f16"),
+])
+def test_int8_small_shapes(ctx, n_out, K, m, gs, xd, y):
+    r = rng(n_out + 3 * K + m)
+    q, _ = int8_weights(r, n_out, K)
+    s = r.uniform(0.001, 0.01, size=(n_out, K // gs)).astype(np.float16)
+    if xd == "f32":
+        Xf = r.standard_normal((m, K)).astype(np.float32)
+        X, xc = Xf, W.F32
+    else:
+        X, Xf, xc = _x(r, m, K, xd)
+    d = W.qdesc(n_out, K, m, 8, gs, 0, W.SCALE_F16, xc, YD[y][0])
+    got = _run(ctx, d, q, s, X, n_out, m, y)
+    # f32 activations are staged as fp16 by this kernel (relative error <= 2^-11 per
+    # activation); the comparison is still against the unrounded fp32 oracle.
+    ref = oracle.matmul_int8_dequant_tokens(q, s.astype(np.float32).reshape(-1),
+                                            Xf.astype(np.float32), gs)
+    compare(got, round_to(ref, y), f"int8 small {n_out}x{K} m{m} g{gs}")
+
+
+@pytest.mark.parametrize("n_out,K,m,gs", [(14336, 4096, 8, 32), (300, 512, 17, 128), (256, 256, 64, 32)])
+def test_int4_small_m(ctx, n_out, K, m, gs):
+    r = rng(n_out + K + 7 * m)
+    q, Wp, s = int4_weights(r, n_out, K, gs)
+    X, Xf, xc = _x(r, m, K, "f16")
+    d = W.qdesc(n_out, K, m, 4, gs, W.NIBBLE_OFFSET_BINARY, W.SCALE_F16, xc, W.F16)
+    got = _run(ctx, d, Wp, s, X, n_out, m, "f16")
+    ref = oracle.matmul_nax_grouped_tokens(Wp, s.astype(np.float32).reshape(-1), Xf, gs)
+    compare(got, round_to(ref, "f16"), f"int4 small m {n_out}x{K} m{m}")

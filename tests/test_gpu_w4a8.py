@@ -1,0 +1,83 @@
+"""GPU parity: W4A8 (int4 weights x int8 activations) through lux_hip_qmatmul.
+
+Oracle: matmul_int4_int8 (quantized.wgsl:590-647, two's-complement nibbles) restated
+in oracle/lux_oracle.c, and its per-group form.  Integer results are compared
+bit-for-bit; the scaled fp output (config 5's group scales and per-token activation
+scales) against the fp64 ground truth rounded to the output dtype.
+"""
+import numpy as np
+import pytest
+
+import oracle
+import webgpu_amd as W
+from util import compare, int4_weights, quantize_rows_int8, rng, round_to
+
+pytestmark = pytest.mark.gpu
+
+
+def _inputs(r, n_out, K, m, gs, coding):
+    q, Wp, s = int4_weights(r, n_out, K, gs, coding)
+    a8, ascale = quantize_rows_int8(r.standard_normal((m, K)).astype(np.float32))
+    return q, Wp, s, a8, ascale
+
+
+@pytest.mark.parametrize("n_out,K,m,coding", [(11008, 4096, 256, 1), (40, 256, 3, 1),
+                                              (97, 512, 300, 0), (64, 128, 17, 1)])
+def test_w4a8_full_k_int32_exact(ctx, n_out, K, m, coding):
+    """Full-K int32 sums (the reference kernel's output), bit-exact."""
+    r = rng(n_out + K + m)
+    q, Wp, s, a8, _ = _inputs(r, n_out, K, m, 128, coding)
+    d = W.qdesc(n_out, K, m, 4, 128, coding, W.SCALE_NONE, W.I8, W.I32)
+    wb, xb, yb = ctx.upload(Wp), ctx.upload(a8), ctx.alloc(m * n_out * 4)
+    ctx.qmatmul(d, wb, None, xb, None, yb)
+    got = ctx.download(yb, np.int32, (m, n_out))
+    ref = oracle.matmul_int4_int8(Wp, np.ascontiguousarray(a8.T), coding).T  # [m, n]
+    assert np.array_equal(got, ref)
+    if n_out * m < 10**6:  # an independent int64 check on the small shapes
+        assert np.array_equal(got, (a8.astype(np.int64) @ q.T).astype(np.int32))
+
+
+@pytest.mark.parametrize("n_out,K,m,gs", [(512, 4096, 256, 128), (70, 512, 20, 256)])
+def test_w4a8_group_partials_exact(ctx, n_out, K, m, gs):
+    """Per-group int32 partial sums, bit-exact against brute force."""
+    r = rng(7 * n_out + m)
+    q, Wp, s, a8, _ = _inputs(r, n_out, K, m, gs, 1)
+    d = W.qdesc(n_out, K, m, 4, gs, 1, W.SCALE_F16, W.I8, W.I32, W.QFLAG_GROUP_PARTIALS)
+    wb, sb, xb = ctx.upload(Wp), ctx.upload(s), ctx.upload(a8)
+    yb = ctx.alloc(m * n_out * (K // gs) * 4)
+    ctx.qmatmul(d, wb, sb, xb, None, yb)
+    got = ctx.download(yb, np.int32, (m, n_out, K // gs))
+    ref = oracle.w4a8_group_partials(Wp, a8, gs, 1)
+    assert np.array_equal(got, ref)
+
+
+@pytest.mark.parametrize("y", ["f16", "f32"])
+def test_config5_scaled(ctx, y):
+    """C5: W 11008 x 4096 int4 g128 fp16 scales, A 256 x 4096 per-token int8."""
+    r = rng(5)
+    n_out, K, m, gs = 11008, 4096, 256, 128
+    q, Wp, s, a8, ascale = _inputs(r, n_out, K, m, gs, 1)
+    ycode, ynp = {"f16": (W.F16, np.float16), "f32": (W.F32, np.float32)}[y]
+    d = W.qdesc(n_out, K, m, 4, gs, 1, W.SCALE_F16, W.I8, ycode)
+    wb, sb, xb, asb = ctx.upload(Wp), ctx.upload(s), ctx.upload(a8), ctx.upload(ascale)
+    yb = ctx.alloc(m * n_out * np.dtype(ynp).itemsize)
+    ctx.qmatmul(d, wb, sb, xb, asb, yb)
+    got = ctx.download(yb, ynp, (m, n_out)).astype(np.float64)
+    P = oracle.w4a8_group_partials(Wp, a8, gs, 1).astype(np.float64)      # [m, n, G]
+    ref = (P * s.astype(np.float64)[None, :, :]).sum(axis=2) * ascale.astype(np.float64)[:, None]
+    st = compare(got, round_to(ref.astype(np.float32), y), f"C5 scaled {y}")
+    print(f"C5 {y} rel-L2 {st['rel_l2']:.3e}")
+
+
+def test_w4a8_rejects(ctx):
+    r = rng(1)
+    q, Wp, s, a8, ascale = _inputs(r, 32, 128, 4, 128, 1)
+    wb, sb, xb, yb = ctx.upload(Wp), ctx.upload(s), ctx.upload(a8), ctx.alloc(4 * 32 * 4)
+    with pytest.raises(W.LuxError) as e:  # fp output needs per-token activation scales
+        ctx.qmatmul(W.qdesc(32, 128, 4, 4, 128, 1, W.SCALE_F16, W.I8, W.F32), wb, sb, xb, None, yb)
+    assert e.value.code == W.LUX_BACKEND_ERROR_INVALID_ARGUMENT
+    s64 = ctx.upload(np.ones((32, 2), np.float16))
+    with pytest.raises(W.LuxError) as e:  # group of 64 does not hold whole 128-k stages
+        ctx.qmatmul(W.qdesc(32, 128, 4, 4, 64, 1, W.SCALE_F16, W.I8, W.F32), wb, s64, xb,
+                    ctx.upload(ascale), yb)
+    assert e.value.code == W.LUX_BACKEND_ERROR_NOT_SUPPORTED

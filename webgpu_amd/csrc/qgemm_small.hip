@@ -1,0 +1,312 @@
+// Weight-only quantized matmul for small m (decode batches, m <= 64 per pass):
+//   Y[m, n] = sum_k (q(n, k) * s(n, k / gs)) * X[m, k]
+// int8 weights (per-row or per-group scales) and int4 weights (group scales).
+//
+// Reference: int8 -- dequantize_nax_int8_group then WGSL_MATMUL
+// (quantized_nax.wgsl:364-386, src/webgpu_plugin.cpp:138-205); int4 --
+// matmul_nax_grouped (quantized_nax.wgsl:568-626).  Config 3 of BASELINE.json:
+// W 28672 x 8192 int8, per-row fp16 scales, X m x 8192 fp16 (m = 8, 32), fp16 out.
+// At 16 to 63 flop per weight byte this is HBM-bound (the MFMA ridge is ~300).
+//
+// Numerics: int8 values are exact in fp16 and so are the fp16 activations, so every
+// MFMA product is exact; the row scale multiplies the fp32 sum at the end (per-group
+// scales multiply fp32 partial sums), which reassociates the reference's
+// sum of (q*s)*x without extra rounding of the weights.  int4 weights are staged as
+// fp16(q*s) (RNE, relative error <= 2^-11), as in the large-m GEMM.
+//
+// Layout (gfx950, v_mfma_f32_16x16x32_f16): A = W rows (16 per wave), B = X^T (16 tokens
+// per m-tile).  Lane l owns weight row l % 16 and k-quarter l / 16: each lane streams
+// 16 contiguous bytes of its row per load straight from HBM into registers (no LDS),
+// decodes them to fp16 and feeds two (int8) or four (int4) MFMA k-steps.  X is staged
+// once per block in LDS, in the element order the decode produces, and shared by the
+// block's waves.  A block is NW waves x 16 rows; the host picks NW so that every CU
+// gets one block when it can (28672 rows on 256 CUs: 7 waves of 16 rows).
+#include <algorithm>
+
+#include "common.hpp"
+
+namespace luxhip {
+
+namespace {
+
+constexpr int KC = 256;            // k per staged X chunk
+constexpr int XROW = KC + 8;       // LDS halves per staged X row (pad: conflict-free reads)
+constexpr int MAXW = 16;           // max waves per block
+
+__device__ __forceinline__ uint32_t pack_h2s(f16 a, f16 b) {
+    return __builtin_bit_cast(uint32_t, f16x2{a, b});
+}
+
+__device__ __forceinline__ uint32_t and_or_s(uint32_t a, uint32_t m, uint32_t o) {
+    uint32_t r;
+    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "s"(m), "v"(o));
+    return r;
+}
+
+// 4 signed bytes -> fp16 (b0, b2, b1, b3), exact: (b ^ 0x80) = b + 128 in [0, 255],
+// (1024 + u) - 1152 = b.
+__device__ __forceinline__ uint2 i8x4_to_f16(uint32_t w, uint32_t magic) {
+    const f16x2 OFF = {(f16)1152.0f, (f16)1152.0f};
+    const uint32_t u = w ^ 0x80808080u;
+    const uint32_t lo = and_or_s(u, 0x00FF00FFu, magic);
+    const uint32_t hi = and_or_s(u >> 8, 0x00FF00FFu, magic);
+    return uint2{__builtin_bit_cast(uint32_t, __builtin_bit_cast(f16x2, lo) - OFF),
+                 __builtin_bit_cast(uint32_t, __builtin_bit_cast(f16x2, hi) - OFF)};
+}
+
+// 8 offset-binary nibbles times an fp16 scale -> fp16(q*s) (RNE) in the order
+// (k, k+4, k+1, k+5, k+2, k+6, k+3, k+7).
+__device__ __forceinline__ f16x8 i4x8_to_f16(uint32_t w, f16x2 s2, uint32_t magic) {
+    const f16x2 OFF = {(f16)1032.0f, (f16)1032.0f};
+    uint32_t o[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t t = and_or_s(w >> (4 * i), 0x000F000Fu, magic);
+        o[i] = __builtin_bit_cast(uint32_t, (__builtin_bit_cast(f16x2, t) - OFF) * s2);
+    }
+    return __builtin_bit_cast(f16x8, u32x4{o[0], o[1], o[2], o[3]});
+}
+
+}  // namespace
+
+// WB: weight bits (8 or 4).  MT: m-tiles of 16 tokens (m <= 16 MT).  PERROW: int8 with
+// one scale per row (applied after the k loop); otherwise int8 scales are applied per
+// 32-k step (group size a multiple of 64) and int4 scales inside the decode.
+template <int WB, int MT, bool PERROW, ScaleKind SK, XKind XK, YKind YK>
+__global__ __launch_bounds__(64 * MAXW) void k_qgemm_small(
+    const uint8_t* __restrict__ W, const void* __restrict__ S, const void* __restrict__ X,
+    void* __restrict__ Y, int M, int N, int K, int gs, uint32_t xor_mask) {
+    __shared__ __attribute__((aligned(16))) f16 xs[2][16 * MT][XROW];
+
+    const int nw = blockDim.x >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int n0 = (blockIdx.x * nw + wv) * 16;
+    const int r16 = lane & 15, kq = lane >> 4;
+    const int G = K / gs;
+    const uint32_t magic = 0x64006400u;
+
+    // ---- X staging: 16*MT rows x KC k per chunk; 8 elements per thread step,
+    // reordered into the decode order and converted to fp16.
+    const int xchunks = 16 * MT * (KC / 8);
+    auto stage_x = [&](int buf, int k0) {
+        for (int c = tid; c < xchunks; c += blockDim.x) {
+            const int row = c / (KC / 8), kc = (c % (KC / 8)) * 8;
+            f16 h[8];
+            if (row < M) {
+#pragma unroll
+                for (int e = 0; e < 8; ++e) h[e] = (f16)load_x<XK>(X, (size_t)row * K + k0 + kc + e);
+            } else {
+#pragma unroll
+                for (int e = 0; e < 8; ++e) h[e] = (f16)0.0f;
+            }
+            u32x4 v;
+            if constexpr (WB == 8)  // (0, 2, 1, 3) inside every 4
+                v = u32x4{pack_h2s(h[0], h[2]), pack_h2s(h[1], h[3]), pack_h2s(h[4], h[6]), pack_h2s(h[5], h[7])};
+            else                    // (0, 4, 1, 5, 2, 6, 3, 7) inside every 8
+                v = u32x4{pack_h2s(h[0], h[4]), pack_h2s(h[1], h[5]), pack_h2s(h[2], h[6]), pack_h2s(h[3], h[7])};
+            *reinterpret_cast<u32x4*>(&xs[buf][row][kc]) = v;
+        }
+    };
+
+    // ---- weight stream: lane (row r16, quarter kq) reads 16 B per load.  int8: a load
+    // covers 64 k (the quarter's 16 bytes = k 16 kq .. 16 kq + 15); int4: 128 k
+    // (32 nibbles = k 32 kq .. 32 kq + 31).
+    constexpr int KPL = WB == 8 ? 64 : 128;    // k per load (whole wave)
+    constexpr int LPC = KC / KPL;              // loads per X chunk
+    const int row = min(n0 + r16, N - 1);
+    const size_t rowbytes = (size_t)K * WB / 8;
+    const uint8_t* wrow = W + (size_t)row * rowbytes + 16 * kq;
+
+    f32x4 acc[MT];
+#pragma unroll
+    for (int t = 0; t < MT; ++t) acc[t] = f32x4{};
+
+    const int nchunks = K / KC;
+    u32x4 wq[2][LPC];                          // two chunks of weights in flight
+    auto load_w = [&](int slot, int chunk) {
+        chunk = min(chunk, nchunks - 1);
+#pragma unroll
+        for (int l = 0; l < LPC; ++l)
+            wq[slot][l] = __builtin_nontemporal_load(
+                reinterpret_cast<const u32x4*>(wrow + (size_t)(chunk * LPC + l) * (KPL * WB / 8)));
+    };
+
+    // One chunk: KC k from X buffer `buf` and weight registers `slot` (static).
+    auto chunk = [&](int c, int buf, int slot) {
+#pragma unroll
+        for (int l = 0; l < LPC; ++l) {
+            const u32x4 q = wq[slot][l];
+            const int kbase = c * KC + l * KPL;   // first k of this load
+            if constexpr (WB == 8) {
+                // two k-steps of 32: bytes 0-7 and 8-15 of the lane's 16
+#pragma unroll
+                for (int st = 0; st < 2; ++st) {
+                    const uint2 p0 = i8x4_to_f16(st ? q.z : q.x, magic);
+                    const uint2 p1 = i8x4_to_f16(st ? q.w : q.y, magic);
+                    const f16x8 a = __builtin_bit_cast(f16x8, u32x4{p0.x, p0.y, p1.x, p1.y});
+#pragma unroll
+                    for (int t = 0; t < MT; ++t) {
+                        const f16x8 b = *reinterpret_cast<const f16x8*>(
+                            &xs[buf][16 * t + r16][l * KPL + 16 * kq + 8 * st]);
+                        if constexpr (PERROW) {
+                            acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, acc[t], 0, 0, 0);
+                        } else {
+                            const f32x4 p = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, f32x4{}, 0, 0, 0);
+                            // D rows 4*(lane/16) + r: scales of those rows for this group
+                            const int g = kbase / gs;
+#pragma unroll
+                            for (int r = 0; r < 4; ++r) {
+                                const int nr = min(n0 + 4 * kq + r, N - 1);
+                                acc[t][r] = fmaf(p[r], load_scale_t<SK>(S, (size_t)nr * G + g), acc[t][r]);
+                            }
+                        }
+                    }
+                }
+            } else {
+                // four k-steps of 32: word w covers k 32 kq + 8 w .. + 7 of this load
+                const int g = (kbase + 32 * kq) / gs;
+                const f16 sc = (f16)load_scale_t<SK>(S, (size_t)row * G + g);
+                const f16x2 s2 = {sc, sc};
+                const uint32_t words[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+                for (int st = 0; st < 4; ++st) {
+                    const f16x8 a = i4x8_to_f16(words[st] ^ xor_mask, s2, magic);
+#pragma unroll
+                    for (int t = 0; t < MT; ++t) {
+                        const f16x8 b = *reinterpret_cast<const f16x8*>(
+                            &xs[buf][16 * t + r16][l * KPL + 32 * kq + 8 * st]);
+                        acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, acc[t], 0, 0, 0);
+                    }
+                }
+            }
+        }
+    };
+
+    // Chunks in pairs so the two weight-register slots are static; weights run two
+    // chunks ahead of use, X one chunk ahead (double-buffered LDS).
+    load_w(0, 0);
+    load_w(1, 1);
+    stage_x(0, 0);
+    __syncthreads();
+    for (int c = 0; c < nchunks; c += 2) {
+        if (c + 1 < nchunks) stage_x(1, (c + 1) * KC);
+        chunk(c, 0, 0);
+        load_w(0, c + 2);
+        __syncthreads();
+        if (c + 1 < nchunks) {
+            if (c + 2 < nchunks) stage_x(0, (c + 2) * KC);
+            chunk(c + 1, 1, 1);
+            load_w(1, c + 3);
+            __syncthreads();
+        }
+    }
+
+    // ---- epilogue: D[i][j] of a 16x16 tile sits in lane j + 16 * (i / 4), register i % 4;
+    // i = weight row (n), j = token (m).
+#pragma unroll
+    for (int t = 0; t < MT; ++t) {
+        const int m = 16 * t + r16;
+        if (m >= M) continue;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int n = n0 + 4 * kq + r;
+            if (n >= N) continue;
+            float v = acc[t][r];
+            if constexpr (WB == 8 && PERROW) v *= load_scale_t<SK>(S, (size_t)n);
+            store_y<YK>(Y, (size_t)m * N + n, v);
+        }
+    }
+}
+
+bool qgemm_small_supported(const QArgs& a) {
+    if (a.x_kind == XKind::I8 || a.y_kind == YKind::I32) return false;
+    if (a.k % KC != 0 || ((uintptr_t)a.w & 15u) != 0) return false;
+    if (a.wbits == 8) {
+        const bool perrow = a.group_size == a.k || a.scale_kind == ScaleKind::None;
+        return perrow || a.group_size % 64 == 0;
+    }
+    return a.wbits == 4 && a.group_size % 32 == 0 && a.scale_kind != ScaleKind::None;
+}
+
+template <int WB, int MT, bool PERROW, ScaleKind SK, XKind XK, YKind YK>
+static void launch_one(const QArgs& a, const void* x, void* y, int m, hipStream_t s) {
+    // Waves per block: the largest count <= 16 that divides the 16-row tiles evenly over
+    // the CUs (one block per CU), else 4.
+    static int cus = 0;
+    if (!cus) {
+        int dev = 0;
+        (void)hipGetDevice(&dev);
+        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) cus = 256;
+    }
+    const int tiles = (a.n_out + 15) / 16;
+    int nw = 4;
+    if (tiles % cus == 0 && tiles / cus <= MAXW) nw = tiles / cus;
+    else if (tiles <= cus * MAXW && tiles >= cus) nw = (tiles + cus - 1) / cus;
+    const dim3 grid((tiles + nw - 1) / nw), block(64 * nw);
+    hipLaunchKernelGGL((k_qgemm_small<WB, MT, PERROW, SK, XK, YK>), grid, block, 0, s,
+                       reinterpret_cast<const uint8_t*>(a.w), a.s, x, y, m, a.n_out, a.k,
+                       a.group_size, a.xor_mask);
+}
+
+template <int WB, bool PERROW, ScaleKind SK, XKind XK, YKind YK>
+static void launch_m(const QArgs& a, hipStream_t s) {
+    // m > 64: passes of 64 tokens (each re-reads the weights).
+    const size_t xel = a.x_kind == XKind::F32 ? 4 : 2;
+    const size_t yel = a.y_kind == YKind::F32 ? 4 : 2;
+    for (int m0 = 0; m0 < a.m; m0 += 64) {
+        const int m = std::min(64, a.m - m0);
+        const void* x = reinterpret_cast<const uint8_t*>(a.x) + (size_t)m0 * a.k * xel;
+        void* y = reinterpret_cast<uint8_t*>(a.y) + (size_t)m0 * a.n_out * yel;
+        if (m <= 16) launch_one<WB, 1, PERROW, SK, XK, YK>(a, x, y, m, s);
+        else if (m <= 32) launch_one<WB, 2, PERROW, SK, XK, YK>(a, x, y, m, s);
+        else if (m <= 48) launch_one<WB, 3, PERROW, SK, XK, YK>(a, x, y, m, s);
+        else launch_one<WB, 4, PERROW, SK, XK, YK>(a, x, y, m, s);
+    }
+}
+
+template <int WB, bool PERROW, ScaleKind SK, XKind XK>
+static bool launch_y(const QArgs& a, hipStream_t s) {
+    switch (a.y_kind) {
+        case YKind::F32: launch_m<WB, PERROW, SK, XK, YKind::F32>(a, s); return true;
+        case YKind::F16: launch_m<WB, PERROW, SK, XK, YKind::F16>(a, s); return true;
+        case YKind::BF16: launch_m<WB, PERROW, SK, XK, YKind::BF16>(a, s); return true;
+        default: return false;
+    }
+}
+
+template <int WB, bool PERROW, ScaleKind SK>
+static bool launch_x(const QArgs& a, hipStream_t s) {
+    switch (a.x_kind) {
+        case XKind::F16: return launch_y<WB, PERROW, SK, XKind::F16>(a, s);
+        case XKind::BF16: return launch_y<WB, PERROW, SK, XKind::BF16>(a, s);
+        case XKind::F32: return launch_y<WB, PERROW, SK, XKind::F32>(a, s);
+        default: return false;
+    }
+}
+
+template <int WB, bool PERROW>
+static bool launch_s(const QArgs& a, hipStream_t s) {
+    switch (a.scale_kind) {
+        case ScaleKind::F16: return launch_x<WB, PERROW, ScaleKind::F16>(a, s);
+        case ScaleKind::F32: return launch_x<WB, PERROW, ScaleKind::F32>(a, s);
+        case ScaleKind::GroupScale: return launch_x<WB, PERROW, ScaleKind::GroupScale>(a, s);
+        case ScaleKind::None:
+            if constexpr (WB == 8 && PERROW) return launch_x<WB, PERROW, ScaleKind::None>(a, s);
+            return false;
+        default: return false;
+    }
+}
+
+hipError_t launch_qgemm_small(const QArgs& a, hipStream_t s) {
+    bool ok;
+    if (a.wbits == 8) {
+        const bool perrow = a.group_size == a.k || a.scale_kind == ScaleKind::None;
+        ok = perrow ? launch_s<8, true>(a, s) : launch_s<8, false>(a, s);
+    } else {
+        ok = launch_s<4, false>(a, s);
+    }
+    if (!ok) return hipErrorInvalidValue;
+    return hipGetLastError();
+}
+
+}  // namespace luxhip

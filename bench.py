@@ -36,6 +36,22 @@ C4_FLOPS = 2 * 2048 * 14336 * 4096
 C3 = dict(n_out=28672, k=8192)
 C5 = dict(n_out=11008, k=4096, m=256, gs=128)
 INT8_MFMA_PEAK_TOPS = 5000.0
+COPY_BYTES = 512 * 2**20
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "hbm_traffic.md")
+
+
+def measured_traffic(key: str):
+    """HBM bytes per launch measured with rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE
+    (scaled by the copy-kernel calibration), recorded in profiles/hbm_traffic.md as
+    a line `traffic <key>: <bytes>`; None when not recorded."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            for line in f:
+                if line.startswith(f"traffic {key}:"):
+                    return int(line.split(":", 1)[1].strip().split()[0])
+    except OSError:
+        pass
+    return None
 
 
 def log(msg):
@@ -164,7 +180,8 @@ def bench_c5(torch, W, ctx, steps, warmup):
     return {"us_per_launch": round(per * 1e6, 2), "value": round(tops, 2), "unit": "TOP/s",
             "hbm_gbs": round(nbytes / per / 1e9, 2),
             "roofline": {"bound": "mfma", "achieved": round(tops, 2), "peak": INT8_MFMA_PEAK_TOPS,
-                         "unit": "TOP/s", "frac": round(tops / INT8_MFMA_PEAK_TOPS, 4), "traffic": None}}
+                         "unit": "TOP/s", "frac": round(tops / INT8_MFMA_PEAK_TOPS, 4),
+                         "traffic": measured_traffic("c5")}}
 
 
 def cpu_baseline_c2(Wp, s, x, budget_s=10.0):
@@ -192,7 +209,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=10.0)
-    ap.add_argument("--only", choices=["c2", "c3", "c4", "c5"], default=None,
+    ap.add_argument("--only", choices=["c2", "c3", "c4", "c5", "copy"], default=None,
                     help="run one config only (profiling); the JSON line needs both")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -210,6 +227,16 @@ def main():
     if args.only == "c4":
         c4 = bench_c4(torch, W, ctx, args.steps, args.warmup)
         log(f"  C4 {c4['per_launch_s']*1e6:.1f} us/launch, {c4['tflops']:.1f} TFLOP/s")
+        return
+    if args.only == "copy":
+        # calibration for the FETCH_SIZE / WRITE_SIZE counters: a plain device copy
+        # of known size (COPY_BYTES read + COPY_BYTES written per launch)
+        src = torch.empty(COPY_BYTES, dtype=torch.uint8, device="cuda").random_(0, 255)
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"  copy {COPY_BYTES} bytes x5 done")
         return
     if args.only == "c3":
         for m in (8, 32):
@@ -268,14 +295,15 @@ def main():
                    "n_out": 14336, "k": 4096, "m": 1, "group_size": 32,
                    "weight_copies_rotated": c2["copies"], "timing": "hip graph of K launches"},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None},
+                     "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
+                     "traffic": measured_traffic("c2")},
         "cpu_baseline": cpu,
         "int4_gemm_m2048": None if c4 is None else {
             "value": round(c4["tflops"], 2), "unit": "TFLOP/s",
             "us_per_launch": round(c4["per_launch_s"] * 1e6, 2),
             "roofline": {"bound": "mfma", "achieved": round(c4["tflops"], 2),
                          "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s",
-                         "frac": round(c4["frac"], 4), "traffic": None}},
+                         "frac": round(c4["frac"], 4), "traffic": measured_traffic("c4")}},
         "int8_gemm_c3": c3s or None,
         "w4a8_gemm_c5": c5,
     }

@@ -9,14 +9,22 @@
 // Output modes (lux_hip_qmatmul descriptor):
 //   y I32, no GROUP_PARTIALS : full-K int32 sums (the reference kernel's output);
 //   y I32, GROUP_PARTIALS    : P[m][n][g] int32 per group (bit-exact checking aid);
-//   y F16/BF16/F32           : the scaled sum above, fp32 accumulation of s * P_g.
+//   y F16/BF16/F32           : the scaled sum above, fp32 accumulation of s * P_g in
+//                              group order g = 0 .. G-1.
 //
-// Layout (gfx950, v_mfma_i32_16x16x64_i8): A = weight rows (16 per wave), B = A8^T
-// (16 tokens per m-tile), K = 64 per instruction.  Per 128-k group a lane (row l % 16,
-// quarter q = l / 16) loads 16 packed bytes = k 32 q .. 32 q + 31 and sign-extends the
-// nibbles into bytes with a SWAR add/xor, in the order (k0 k2 k4 k6 | k1 k3 k5 k7) per 8;
-// the two MFMA k-steps of the group take nibbles 0-15 and 16-31.  Activations are
-// staged per block in LDS with the same byte order.  int32 accumulation is exact.
+// Tiling (gfx950, v_mfma_i32_16x16x64_i8, A = weight rows, B = tokens, K = 64):
+//   block = 4 waves = 128 weight rows x 64 tokens; wave = 32 rows (2 row tiles) x 64
+//   tokens (4 token tiles).  Per 128-k stage a lane (row l % 16, quarter q = l / 16)
+//   loads 16 packed bytes per row tile = k 32 q .. 32 q + 31 and sign-extends the
+//   nibbles into bytes with a SWAR add/xor, in the order (k0 k2 k4 k6 | k1 k3 k5 k7)
+//   per 8 k; the two MFMA k-steps take nibbles 0-15 and 16-31.  Activations of the
+//   stage (64 tokens x 128 B) are loaded as coalesced 16-B chunks one stage ahead,
+//   byte-permuted into the same order and written to LDS; all four waves read them.
+//   The weights are the only operand each wave owns, so nothing is decoded twice.
+//
+// Block order is XCD-aware: consecutive workgroups go to the 8 XCDs in turn, so the
+// token blocks of one row block are given block ids that land on the same XCD and
+// share its L2 copy of the 128 weight rows.
 #include <algorithm>
 
 #include "common.hpp"
@@ -25,16 +33,22 @@ namespace luxhip {
 
 namespace {
 
-constexpr int GK = 128;            // k per stage (one group of 128 when gs == 128)
-constexpr int AROW = GK + 16;      // LDS bytes per staged activation row (padded)
-constexpr int BT = 256;            // tokens per block (m tile of the block)
+constexpr int GK = 128;    // k per stage (one group of 128 when gs == 128)
+constexpr int AROW = GK + 16;  // LDS bytes per staged token row (padded)
+constexpr int BR = 128;    // weight rows per block
+constexpr int BT = 64;     // tokens per block
+constexpr int NXCD = 8;
+constexpr int PD = 4;      // stages fetched ahead
+constexpr int GMAX = 128;  // groups per row held in LDS (scaled output)
+constexpr int SCH = 16;    // 16-byte scale chunks per thread (block region <= 64 KB)
 
-// 8 offset-binary nibbles (k0..k7) -> two words of signed bytes
-// (k0, k2, k4, k6) and (k1, k3, k5, k7): byte = ((u + 0x78) ^ 0x80) with u = q + 8.
-__device__ __forceinline__ void unpack_i4_to_i8(uint32_t w, uint32_t& lo, uint32_t& hi) {
+// 8 nibbles (k0..k7) of one word -> signed bytes (k0, k2, k4, k6) and (k1, k3, k5, k7).
+// Offset-binary u = q + 8: byte = (u + 0x78) ^ 0x80.  Two's complement t: u = t ^ 8,
+// folded in through `tc` (0x08080808 for two's complement, 0 for offset-binary).
+__device__ __forceinline__ void unpack_i4_to_i8(uint32_t w, uint32_t tc, uint32_t& lo, uint32_t& hi) {
     const uint32_t u0 = w & 0x0F0F0F0Fu, u1 = (w >> 4) & 0x0F0F0F0Fu;
-    lo = (u0 + 0x78787878u) ^ 0x80808080u;
-    hi = (u1 + 0x78787878u) ^ 0x80808080u;
+    lo = ((u0 ^ tc) + 0x78787878u) ^ 0x80808080u;
+    hi = ((u1 ^ tc) + 0x78787878u) ^ 0x80808080u;
 }
 
 // 8 activation bytes (a0..a7 as two words) -> (a0 a2 a4 a6) (a1 a3 a5 a7).
@@ -44,130 +58,252 @@ __device__ __forceinline__ void perm_bytes(uint32_t x, uint32_t y, uint32_t& lo,
     hi = __builtin_amdgcn_perm(y, x, 0x07050301u);
 }
 
+__device__ __forceinline__ u32x4 perm16(u32x4 v) {
+    uint32_t a, b, c, d;
+    perm_bytes(v.x, v.y, a, b);
+    perm_bytes(v.z, v.w, c, d);
+    return u32x4{a, b, c, d};
+}
+
+template <YKind YK>
+__device__ __forceinline__ void store4(void* Y, size_t idx, f32x4 v, bool vec) {
+    if (vec) {
+        if constexpr (YK == YKind::F32) {
+            *reinterpret_cast<f32x4*>(static_cast<float*>(Y) + idx) = v;
+        } else if constexpr (YK == YKind::F16) {
+            const f16x4 h = {(_Float16)v[0], (_Float16)v[1], (_Float16)v[2], (_Float16)v[3]};
+            *reinterpret_cast<f16x4*>(static_cast<_Float16*>(Y) + idx) = h;
+        } else {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) store_y<YK>(Y, idx + r, v[r]);
+        }
+    } else {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) store_y<YK>(Y, idx + r, v[r]);
+    }
+}
+
 }  // namespace
 
 // MODE 0: full-K int32; 1: per-group int32 partials; 2: scaled fp output.
-template <int MODE, int MT, ScaleKind SK, YKind YK>
-__global__ __launch_bounds__(256) void k_w4a8(const uint32_t* __restrict__ W,
+// ONEG: group size == 128, every stage is one whole group (no carry across stages).
+template <int MODE, bool ONEG, ScaleKind SK, YKind YK>
+__global__ __launch_bounds__(256) void k_w4a8(const uint8_t* __restrict__ W,
                                               const void* __restrict__ S,
                                               const int8_t* __restrict__ A,
                                               const float* __restrict__ AS,
                                               void* __restrict__ Y, int M, int N, int K, int gs,
-                                              uint32_t xor_mask) {
+                                              uint32_t tc, int nrb, int ntb, int vec_y) {
     __shared__ __attribute__((aligned(16))) uint8_t as[2][BT][AROW];
+    extern __shared__ __attribute__((aligned(16))) float ssT[];  // MODE 2: [G][BR] scales
 
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-    // block: 32 weight rows x BT tokens; wave: 16 rows (wv & 1) x 16*MT tokens (wv >> 1)
-    const int n0 = blockIdx.x * 32 + (wv & 1) * 16;
-    const int tb = blockIdx.y * BT;                    // first token of the block
-    const int t0 = (wv >> 1) * 16 * MT;                // first token of the wave (in block)
+    const int b = blockIdx.x, j = b / NXCD;
+    const int rb = (j / ntb) * NXCD + b % NXCD, tbk = j % ntb;
+    if (rb >= nrb) return;  // whole block: no barrier is skipped by part of it
+    const int n0 = rb * BR + wv * 32;  // first weight row of the wave
+    const int tb = tbk * BT;           // first token of the block
     const int r16 = lane & 15, q = lane >> 4;
     const int G = K / gs;
-    const int row = min(n0 + r16, N - 1);
-    const uint8_t* wrow = reinterpret_cast<const uint8_t*>(W) + (size_t)row * (K / 2) + 16 * q;
+    const int nst = K / GK;
 
-    // ---- activation staging: BT tokens x GK bytes; thread t stages token t (8 x 16 B)
-    auto stage_a = [&](int buf, int k0) {
-        const int tok = tb + tid;
-        uint8_t* dst = &as[buf][tid][0];
-        if (tok < M) {
-            const u32x4* src = reinterpret_cast<const u32x4*>(A + (size_t)tok * K + k0);
-#pragma unroll
-            for (int c = 0; c < GK / 16; ++c) {
-                const u32x4 v = src[c];
-                uint32_t a, b, cc, d;
-                perm_bytes(v.x, v.y, a, b);
-                perm_bytes(v.z, v.w, cc, d);
-                *reinterpret_cast<u32x4*>(dst + 16 * c) = u32x4{a, b, cc, d};
-            }
-        } else {
-#pragma unroll
-            for (int c = 0; c < GK / 16; ++c) *reinterpret_cast<u32x4*>(dst + 16 * c) = u32x4{0u, 0u, 0u, 0u};
-        }
+    // Raw buffer loads: each lane keeps a fixed byte offset (voffset) and the stage
+    // moves a uniform offset (soffset, scalar arithmetic only).  Reads past the end of
+    // a buffer return zeros, so rows >= N and tokens >= M need no clamping (their
+    // results are never stored); prefetches past the last stage read harmless data.
+    const __amdgpu_buffer_rsrc_t rw =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(W), (short)0, (int)((size_t)N * K / 2), 0x00020000);
+    const __amdgpu_buffer_rsrc_t ra =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<int8_t*>(A), (short)0, (int)((size_t)M * K), 0x00020000);
+    const int wv0 = (n0 + r16) * (K / 2) + 16 * q, wv1 = wv0 + 16 * (K / 2);
+    // activation chunks of a stage: 64 tokens x 8 chunks of 16 B; thread: token tid / 8
+    // and tid / 8 + 32, chunk tid % 8 (8 lanes read one token's 128 contiguous bytes)
+    const int tk = tid >> 3, part = tid & 7;
+    const int av0 = (tb + tk) * K + 16 * part, av1 = av0 + 32 * K;
+
+    auto ldw = [&](u32x4 (&w)[2], int st) {
+        const int so = __builtin_amdgcn_readfirstlane(st * (GK / 2));
+        w[0] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rw, wv0, so, 0));
+        w[1] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rw, wv1, so, 0));
+    };
+    auto lda = [&](u32x4 (&a)[2], int st) {
+        const int so = __builtin_amdgcn_readfirstlane(st * GK);
+        a[0] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(ra, av0, so, 0));
+        a[1] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(ra, av1, so, 0));
+    };
+    auto sta = [&](int buf, const u32x4 (&a)[2]) {
+        *reinterpret_cast<u32x4*>(&as[buf][tk][16 * part]) = perm16(a[0]);
+        *reinterpret_cast<u32x4*>(&as[buf][tk + 32][16 * part]) = perm16(a[1]);
     };
 
-    i32x4 iacc[MT];
-    f32x4 facc[MT];
+    i32x4 iacc[2][4];
+    f32x4 facc[2][4];
 #pragma unroll
-    for (int t = 0; t < MT; ++t) {
-        iacc[t] = i32x4{0, 0, 0, 0};
-        facc[t] = f32x4{};
-    }
+    for (int f = 0; f < 2; ++f)
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            iacc[f][t] = i32x4{0, 0, 0, 0};
+            facc[f][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+        }
 
-    const int nst = K / GK;
-    u32x4 wq = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wrow));
-    stage_a(0, 0);
+    // The block's group scales (rows rb * BR .. + BR - 1 of [N][G]: one contiguous
+    // region) are loaded first, then the first PD stages; then the scales are
+    // converted to fp32 and transposed into ssT[g][row] (rows past N read zeros).
+    u32x4 sv[SCH];
+    constexpr int SB = SK == ScaleKind::F16 ? 2 : SK == ScaleKind::GroupScale ? 16 : 4;
+    constexpr int EPC = SK == ScaleKind::F16 ? 8 : SK == ScaleKind::GroupScale ? 1 : 4;  // per 16 B
+    const int nch = BR * G * SB / 16;
+    if constexpr (MODE == 2) {
+        const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<void*>(S), (short)0, (int)((size_t)N * G * SB), 0x00020000);
+        const int base = rb * BR * G * SB;
+#pragma unroll
+        for (int c = 0; c < SCH; ++c) {
+            const int ch = tid + 256 * c;
+            // unconditional: chunks past the region are read but never used
+            sv[c] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, base + 16 * ch, 0, 0));
+        }
+    }
+    // Weights and activations of stage st + PD are fetched while stage st computes:
+    // PD register sets, the loop unrolled by PD so each set is a fixed set of
+    // registers.  Set i: W[i] holds the weights of the stage it serves; A[i] its
+    // activations, written to LDS at the end of the previous stage.
+    u32x4 Wr[PD][2], Ar[PD][2];
+#pragma unroll
+    for (int i = 0; i < PD; ++i) {
+        ldw(Wr[i], i);
+        lda(Ar[i], i);
+    }
+    if constexpr (MODE == 2) {
+#pragma unroll
+        for (int c = 0; c < SCH; ++c) {
+            const int ch = tid + 256 * c;
+            if (ch < nch) {
+#pragma unroll
+                for (int e = 0; e < EPC; ++e) {
+                    const int idx = ch * EPC + e, row = idx / G, g = idx % G;
+                    const uint32_t wd = sv[c][SK == ScaleKind::F16 ? e / 2 : e];
+                    const uint32_t raw = SK == ScaleKind::F16 ? (wd >> (16 * (e & 1))) & 0xFFFFu : wd;
+                    ssT[g * BR + row] = scale_from_raw<SK>(raw);
+                }
+            }
+        }
+    }
+    sta(0, Ar[0]);
     __syncthreads();
-    for (int st = 0; st < nst; ++st) {
+
+    auto stage = [&](int st, u32x4 (&wc)[2], u32x4 (&ac)[2], const u32x4 (&an)[2]) {
         const int buf = st & 1;
         const int k0 = st * GK;
-        u32x4 wn = wq;
-        if (st + 1 < nst) {
-            wn = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wrow + (size_t)(st + 1) * (GK / 2)));
-            stage_a(buf ^ 1, k0 + GK);
-        }
-        // weights of this stage: k 32 q .. 32 q + 31 -> two k-steps of 16 bytes each
-        uint32_t b8[8];
-        const uint32_t wwords[4] = {wq.x ^ xor_mask, wq.y ^ xor_mask, wq.z ^ xor_mask, wq.w ^ xor_mask};
+        const bool gstart = ONEG || k0 % gs == 0, gend = ONEG || (k0 + GK) % gs == 0;
+        const int g = ONEG ? st : k0 / gs;
+        uint32_t b8[2][8];
+        {
+            const uint32_t ww[2][4] = {{wc[0].x, wc[0].y, wc[0].z, wc[0].w},
+                                       {wc[1].x, wc[1].y, wc[1].z, wc[1].w}};
 #pragma unroll
-        for (int i = 0; i < 4; ++i) unpack_i4_to_i8(wwords[i], b8[2 * i], b8[2 * i + 1]);
-        // A group spans gs / 128 stages: the int32 partial is carried across them and
-        // emitted (MODE 1) or scaled into fp32 (MODE 2) at the group's last stage.
-        const bool gstart = k0 % gs == 0, gend = (k0 + GK) % gs == 0;
-        float sr[4] = {1.f, 1.f, 1.f, 1.f};
+            for (int f = 0; f < 2; ++f)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) unpack_i4_to_i8(ww[f][i], tc, b8[f][2 * i], b8[f][2 * i + 1]);
+        }
+        ldw(wc, st + PD);
+        lda(ac, st + PD);
+        // B fragments of the 4 token tiles, then 8 independent MFMA chains (k-step 0 of
+        // every tile before k-step 1), then the per-group epilogue of each tile.
+        i32x4 bk[4][2];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            const uint8_t* arow = &as[buf][16 * t + r16][32 * q];
+            bk[t][0] = *reinterpret_cast<const i32x4*>(arow);
+            bk[t][1] = *reinterpret_cast<const i32x4*>(arow + 16);
+        }
+        f32x4 sc[2];
         if constexpr (MODE == 2) {
-            if (gend) {
-                const int g = k0 / gs;
+            // scales of this lane's D rows 16 f + 4 q + r for the group
 #pragma unroll
-                for (int r = 0; r < 4; ++r)
-                    sr[r] = load_scale_t<SK>(S, (size_t)min(n0 + 4 * q + r, N - 1) * G + g);
-            }
+            for (int f = 0; f < 2; ++f) sc[f] = *reinterpret_cast<const f32x4*>(&ssT[g * BR + wv * 32 + 16 * f + 4 * q]);
         }
+        i32x4 p[2][4];
 #pragma unroll
-        for (int t = 0; t < MT; ++t) {
-            const uint8_t* arow = &as[buf][t0 + 16 * t + r16][32 * q];
-            i32x4 p = (MODE == 0 || !gstart) ? iacc[t] : i32x4{0, 0, 0, 0};
+        for (int t = 0; t < 4; ++t)
 #pragma unroll
-            for (int ks = 0; ks < 2; ++ks) {
-                const i32x4 a = i32x4{(int)b8[4 * ks], (int)b8[4 * ks + 1], (int)b8[4 * ks + 2], (int)b8[4 * ks + 3]};
-                const i32x4 b = *reinterpret_cast<const i32x4*>(arow + 16 * ks);
-                p = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, p, 0, 0, 0);
-            }
-            iacc[t] = p;
-            if constexpr (MODE == 1) {
-                // P[m][n][g]: D[i][j] = lane j + 16 (i / 4), register i % 4; i = row, j = token
-                const int m = tb + t0 + 16 * t + r16;
-                const int g = k0 / gs;
-                if (gend && m < M) {
+            for (int f = 0; f < 2; ++f) p[f][t] = (MODE == 0 || !gstart) ? iacc[f][t] : i32x4{0, 0, 0, 0};
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) {
-                        const int n = n0 + 4 * q + r;
-                        if (n < N) reinterpret_cast<int32_t*>(Y)[((size_t)m * N + n) * G + g] = p[r];
+        for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+            for (int t = 0; t < 4; ++t)
+#pragma unroll
+                for (int f = 0; f < 2; ++f) {
+                    const i32x4 a = i32x4{(int)b8[f][4 * ks], (int)b8[f][4 * ks + 1], (int)b8[f][4 * ks + 2],
+                                          (int)b8[f][4 * ks + 3]};
+                    p[f][t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, bk[t][ks], p[f][t], 0, 0, 0);
+                }
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+            for (int f = 0; f < 2; ++f) {
+                if (MODE == 0 || !ONEG) iacc[f][t] = p[f][t];
+                if constexpr (MODE == 1) {
+                    // P[m][n][g]: D row (weight) 16 f + 4 q + r, column (token) r16
+                    const int m = tb + 16 * t + r16;
+                    if (gend && m < M) {
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) {
+                            const int n = n0 + 16 * f + 4 * q + r;
+                            if (n < N) reinterpret_cast<int32_t*>(Y)[((size_t)m * N + n) * G + g] = p[f][t][r];
+                        }
+                    }
+                } else if constexpr (MODE == 2) {
+                    if (gend) {
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) facc[f][t][r] = fmaf((float)p[f][t][r], sc[f][r], facc[f][t][r]);
                     }
                 }
-            } else if constexpr (MODE == 2) {
-                if (gend) {
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) facc[t][r] = fmaf((float)p[r], sr[r], facc[t][r]);
-                }
             }
-        }
-        wq = wn;
+        sta(buf ^ 1, an);  // buf ^ 1 was last read before the previous barrier
         __syncthreads();
+    };
+
+    int st = 0;
+    for (; st + PD <= nst; st += PD) {
+#pragma unroll
+        for (int i = 0; i < PD; ++i) stage(st + i, Wr[i], Ar[i], Ar[(i + 1) % PD]);
     }
+#pragma unroll
+    for (int i = 0; i < PD; ++i)
+        if (st + i < nst) stage(st + i, Wr[i], Ar[i], Ar[(i + 1) % PD]);
 
     if constexpr (MODE != 1) {
+        const bool vec_n = vec_y != 0;  // N % 4 == 0 and Y 16-byte aligned
 #pragma unroll
-        for (int t = 0; t < MT; ++t) {
-            const int m = tb + t0 + 16 * t + r16;
+        for (int t = 0; t < 4; ++t) {
+            const int m = tb + 16 * t + r16;
             if (m >= M) continue;
             const float asc = MODE == 2 ? AS[m] : 1.0f;
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int n = n0 + 4 * q + r;
+            for (int f = 0; f < 2; ++f) {
+                const int n = n0 + 16 * f + 4 * q;
                 if (n >= N) continue;
-                if constexpr (MODE == 0) reinterpret_cast<int32_t*>(Y)[(size_t)m * N + n] = iacc[t][r];
-                else store_y<YK>(Y, (size_t)m * N + n, facc[t][r] * asc);
+                const bool full = vec_n && n + 3 < N;
+                if constexpr (MODE == 0) {
+                    int32_t* y = reinterpret_cast<int32_t*>(Y) + (size_t)m * N + n;
+                    if (full) {
+                        *reinterpret_cast<i32x4*>(y) = iacc[f][t];
+                    } else {
+#pragma unroll
+                        for (int r = 0; r < 4; ++r)
+                            if (n + r < N) y[r] = iacc[f][t][r];
+                    }
+                } else {
+                    const f32x4 v = facc[f][t] * asc;
+                    if (full) {
+                        store4<YK>(Y, (size_t)m * N + n, v, true);
+                    } else {
+#pragma unroll
+                        for (int r = 0; r < 4; ++r)
+                            if (n + r < N) store_y<YK>(Y, (size_t)m * N + n + r, v[r]);
+                    }
+                }
             }
         }
     }
@@ -178,18 +314,43 @@ bool w4a8_supported(const QArgs& a) {
     if (a.wbits != 4 || a.x_kind != XKind::I8) return false;
     if (a.k % GK != 0 || a.group_size % GK != 0) return false;
     if (((uintptr_t)a.w & 15u) != 0 || ((uintptr_t)a.x & 15u) != 0) return false;
+    // byte offsets of the buffer loads are 31-bit
+    const size_t lim = (size_t)1 << 31;
+    if ((size_t)(a.n_out + BR) * a.k / 2 >= lim || (size_t)(a.m + BT) * a.k >= lim) return false;
+    if ((size_t)(a.n_out + BR) * (a.k / a.group_size) * 16 >= lim) return false;
     if (a.y_kind == YKind::I32) return true;  // raw sums or per-group partials: no scales used
-    return a.scale_kind != ScaleKind::None && a.xs != nullptr;
+    // scaled output: the block's scales are staged in LDS (at most GMAX groups per row)
+    const int G = a.k / a.group_size;
+    const int sb = a.scale_kind == ScaleKind::F16 ? 2 : a.scale_kind == ScaleKind::GroupScale ? 16 : 4;
+    return a.scale_kind != ScaleKind::None && a.xs != nullptr && G <= GMAX && BR * G * sb <= 256 * 16 * SCH;
+}
+
+template <int MODE, bool ONEG, ScaleKind SK, YKind YK>
+static void launch_g(const QArgs& a, hipStream_t s) {
+    const int nrb = (a.n_out + BR - 1) / BR, ntb = (a.m + BT - 1) / BT;
+    const int nrb8 = (nrb + NXCD - 1) / NXCD * NXCD;  // row blocks padded to whole XCD rounds
+    const dim3 grid(nrb8 * ntb), block(256);
+    // two's complement nibbles become offset-binary with a xor of 8 per nibble
+    const uint32_t tc = a.xor_mask ? 0x08080808u : 0u;
+    const size_t smem = MODE == 2 ? (size_t)BR * (a.k / a.group_size) * sizeof(float) : 0;
+    if (smem > 48 * 1024) {
+        static bool raised = false;  // once per instantiation
+        if (!raised) {
+            (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&k_w4a8<MODE, ONEG, SK, YK>),
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, BR * GMAX * (int)sizeof(float));
+            raised = true;
+        }
+    }
+    hipLaunchKernelGGL((k_w4a8<MODE, ONEG, SK, YK>), grid, block, smem, s, reinterpret_cast<const uint8_t*>(a.w),
+                       a.s, reinterpret_cast<const int8_t*>(a.x), a.xs, a.y, a.m, a.n_out, a.k,
+                       a.group_size, tc, nrb, ntb,
+                       (a.n_out % 4 == 0 && ((uintptr_t)a.y & 15u) == 0) ? 1 : 0);
 }
 
 template <int MODE, ScaleKind SK, YKind YK>
 static void launch_t(const QArgs& a, hipStream_t s) {
-    constexpr int MT = BT / 2 / 16;  // 8 m-tiles of 16 tokens per wave
-    const dim3 grid((a.n_out + 31) / 32, (a.m + BT - 1) / BT), block(256);
-    hipLaunchKernelGGL((k_w4a8<MODE, MT, SK, YK>), grid, block, 0, s,
-                       reinterpret_cast<const uint32_t*>(a.w), a.s,
-                       reinterpret_cast<const int8_t*>(a.x), a.xs, a.y, a.m, a.n_out, a.k,
-                       a.group_size, a.xor_mask);
+    if (MODE != 0 && a.group_size == GK) return launch_g<MODE, true, SK, YK>(a, s);
+    return launch_g<MODE, false, SK, YK>(a, s);
 }
 
 template <ScaleKind SK>

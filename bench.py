@@ -131,6 +131,31 @@ def bench_c4(torch, W, ctx, steps, warmup):
     return {"per_launch_s": per, "tflops": tf, "frac": tf / MFMA_F16_PEAK_TFLOPS, "steps": n}
 
 
+C1_BYTES = 4096 * 4096 * 4 + 4096 * 4 + 4096 * 4  # W + x read, y written: 67,141,632
+
+
+def bench_c1(torch, W, ctx, steps, warmup):
+    """Config 1 through the ABI's own slot: op_matmul_f32(W, x, y, M=4096, K=4096, N=1)."""
+    r = np.random.default_rng(1)
+    A = (r.standard_normal((4096, 4096)) * 0.02).astype(np.float32)
+    x = r.standard_normal(4096).astype(np.float32)
+    copies = max(2, -(-512 * 2**20 // A.nbytes))
+    abs_ = [ctx.upload(A) for _ in range(copies)]
+    xb, yb = ctx.upload(x), ctx.alloc(4096 * 4)
+
+    def launch(i):
+        ctx.matmul_f32(abs_[i % copies], xb, yb, 4096, 4096, 1)
+
+    n = max(3, min(steps, 100))
+    per = timed_graph(torch, ctx, launch, n, max(1, warmup // 4)) / n
+    for b in abs_:
+        b.free()
+    gbs = C1_BYTES / per / 1e9
+    return {"us_per_launch": round(per * 1e6, 2), "value": round(gbs, 2), "unit": "GB/s",
+            "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS,
+                         "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None}}
+
+
 def c3_bytes(m):
     """Algorithmic HBM bytes of one config-3 call: int8 W + fp16 row scales + X + Y."""
     return C3["n_out"] * C3["k"] + C3["n_out"] * 2 + m * C3["k"] * 2 + m * C3["n_out"] * 2
@@ -209,7 +234,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=10.0)
-    ap.add_argument("--only", choices=["c2", "c3", "c4", "c5", "copy"], default=None,
+    ap.add_argument("--only", choices=["c1", "c2", "c3", "c4", "c5", "copy"], default=None,
                     help="run one config only (profiling); the JSON line needs both")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -238,6 +263,10 @@ def main():
         torch.cuda.synchronize()
         log(f"  copy {COPY_BYTES} bytes x5 done")
         return
+    if args.only == "c1":
+        c1 = bench_c1(torch, W, ctx, args.steps, args.warmup)
+        log(f"  C1 {c1['us_per_launch']} us/launch, {c1['value']} GB/s")
+        return
     if args.only == "c3":
         for m in (8, 32):
             c3 = bench_c3(torch, W, ctx, m, args.steps, args.warmup)
@@ -259,8 +288,11 @@ def main():
         log(f"  C4 {c4['per_launch_s']*1e6:.1f} us/launch, {c4['tflops']:.1f} TFLOP/s")
     except W.LuxError as e:
         log(f"  C4 skipped: {e}")
-    c3s, c5 = [], None
+    c1, c3s, c5 = None, [], None
     try:
+        log("bench: config 1 fp32 GEMV through op_matmul_f32")
+        c1 = bench_c1(torch, W, ctx, args.steps, args.warmup)
+        log(f"  C1 {c1['us_per_launch']} us/launch, {c1['value']} GB/s")
         log("bench: config 3 int8 GEMM M=8,32")
         for m in (8, 32):
             c3s.append(bench_c3(torch, W, ctx, m, args.steps, args.warmup))
@@ -269,7 +301,7 @@ def main():
         c5 = bench_c5(torch, W, ctx, args.steps, args.warmup)
         log(f"  C5 {c5['us_per_launch']} us/launch, {c5['value']} TOP/s")
     except W.LuxError as e:
-        log(f"  C3/C5 skipped: {e}")
+        log(f"  C1/C3/C5 skipped: {e}")
     cpu = None
     if not args.no_cpu_baseline:
         log("bench: CPU baseline (oracle)")
@@ -304,6 +336,7 @@ def main():
             "roofline": {"bound": "mfma", "achieved": round(c4["tflops"], 2),
                          "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s",
                          "frac": round(c4["frac"], 4), "traffic": measured_traffic("c4")}},
+        "fp32_gemv_c1": c1,
         "int8_gemm_c3": c3s or None,
         "w4a8_gemm_c5": c5,
     }

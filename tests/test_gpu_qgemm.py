@@ -156,3 +156,28 @@ def test_int4_small_m(ctx, n_out, K, m, gs):
     got = _run(ctx, d, Wp, s, X, n_out, m, "f16")
     ref = oracle.matmul_nax_grouped_tokens(Wp, s.astype(np.float32).reshape(-1), Xf, gs)
     compare(got, round_to(ref, "f16"), f"int4 small m {n_out}x{K} m{m}")
+
+
+@pytest.mark.parametrize("m,xd", [(300, "bf16"), (8, "bf16"), (8, "f32"), (70, "f32")])
+def test_int4_wide_range_activations(ctx, m, xd):
+    """Rows far outside fp16's normal range (x 3e5 with one element at 3e6, and x 1e-7).
+    bf16 / fp32 activations are staged as fp16 after dividing each row by a power of
+    two, so every row keeps its precision; checked row by row."""
+    r = rng(77 + m)
+    n_out, K, gs = 512, 1024, 32
+    q, Wp, s = int4_weights(r, n_out, K, gs)
+    xf = r.standard_normal((m, K)).astype(np.float32)
+    xf[0] *= 3e5
+    xf[1] *= 1e-7
+    xf[2, 5] = 3e6
+    if xd == "bf16":
+        X = bf16_bits(xf)
+        Xf, xc = bf16_to_f32(X), W.BF16
+    else:
+        X, Xf, xc = xf, xf, W.F32
+    d = W.qdesc(n_out, K, m, 4, gs, W.NIBBLE_OFFSET_BINARY, W.SCALE_F16, xc, W.F32)
+    got = _run(ctx, d, Wp, s, X, n_out, m, "f32")
+    ref = oracle.matmul_nax_grouped_tokens(Wp, s.astype(np.float32).reshape(-1), Xf, gs)
+    assert np.all(np.isfinite(got))
+    for i in range(m):
+        compare(got[i], ref[i].astype(np.float64), f"wide-range row {i} m{m} {xd}")

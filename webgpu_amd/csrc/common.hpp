@@ -94,6 +94,33 @@ __device__ __forceinline__ float load_x(const void* x, size_t idx) {
     else return (float)reinterpret_cast<const int8_t*>(x)[idx];
 }
 
+// ---- fp16 staging of wide activations ---------------------------------------
+// Kernels that feed bf16 / fp32 activations to fp16 MFMAs scale each activation row by
+// a power of two first: fac = 2^(E - 14) with 2^E <= max|x| < 2^(E+1), so x / fac has
+// its maximum in [2^14, 2^15), inside fp16's normal range (max 65504); dividing by fac
+// and multiplying the row's output by fac are exact.  Rows that are all zero or
+// subnormal, or that hold Inf/NaN, keep fac = 1 (an Inf/NaN input then propagates).
+// `mx` is the largest |x| bit pattern of the row (sign cleared) and `mant` the
+// mantissa width of the source type (7 for bf16, 23 for fp32).
+__device__ __forceinline__ float row_pow2_factor(uint32_t mx, int mant) {
+    const int ex = (int)((mx >> mant) & 0xFFu);
+    if (ex == 0 || ex == 0xFF) return 1.0f;
+    return ldexpf(1.0f, max(ex - 141, -126));
+}
+
+// Block-wide max of a per-thread value; `red` is __shared__ scratch of >= 16 words.
+__device__ __forceinline__ uint32_t block_max_u32(uint32_t v, uint32_t* red) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = max(v, (uint32_t)__shfl_xor((int)v, o, 64));
+    const int wv = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) red[wv] = v;
+    __syncthreads();
+    uint32_t r = 0;
+    for (int i = 0; i < (int)(blockDim.x >> 6); ++i) r = max(r, red[i]);
+    __syncthreads();
+    return r;
+}
+
 // Butterfly sum across the 64 lanes of a wave (every lane gets the total).
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
@@ -116,6 +143,7 @@ struct QArgs {
     int group_size;
     int wbits;            // 4 or 8
     uint32_t xor_mask;    // 0x88888888 turns two's-complement nibbles into offset-binary
+    const float* xfac;    // per-row power-of-two factors of staged activations (set by launchers)
     ScaleKind scale_kind;
     XKind x_kind;
     YKind y_kind;
@@ -134,7 +162,9 @@ hipError_t launch_gemv_f16(const void* A, const void* x, float* y, int M, int K,
 hipError_t launch_qgemv_i4(const QArgs& a, hipStream_t s);
 // Weight-only int4/int8 matmul for small m (bandwidth regime), fp16/bf16/f32 X.
 bool qgemm_small_supported(const QArgs& a);
-hipError_t launch_qgemm_small(const QArgs& a, hipStream_t s);
+// workspace: qgemm_small_workspace(a) bytes (per-row activation factors; 0 for fp16 X)
+size_t qgemm_small_workspace(const QArgs& a);
+hipError_t launch_qgemm_small(const QArgs& a, void* workspace, hipStream_t s);
 // int4 grouped GEMM for large m (MFMA regime).  Needs a device workspace of
 // qgemm_i4_large_workspace(a) bytes (X restaged as fp16), 16-byte aligned.
 bool qgemm_i4_large_supported(const QArgs& a);

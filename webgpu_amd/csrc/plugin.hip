@@ -519,13 +519,19 @@ LUX_EXPORT LuxBackendError lux_hip_qmatmul(LuxBackendContext* ctx, const LuxHipQ
         he = launch_qgemv_i4(a, c->stream);
     } else if (M <= 64 && qgemm_small_supported(a)) {
         // decode batches: bandwidth regime, weights streamed once per 64 tokens
-        he = launch_qgemm_small(a, c->stream);
+        const size_t wsb = qgemm_small_workspace(a);
+        void* ws = wsb ? ensure_workspace(c, wsb) : nullptr;
+        if (wsb && !ws) return fail(LUX_BACKEND_ERROR_OUT_OF_MEMORY, "qmatmul: workspace allocation failed");
+        he = launch_qgemm_small(a, ws, c->stream);
     } else if (d->weight_bits == 4 && qgemm_i4_large_supported(a)) {
         void* ws = ensure_workspace(c, qgemm_i4_large_workspace(a));
         if (!ws) return fail(LUX_BACKEND_ERROR_OUT_OF_MEMORY, "qmatmul: workspace allocation failed");
         he = launch_qgemm_i4_large(a, ws, c->stream);
     } else if (qgemm_small_supported(a)) {
-        he = launch_qgemm_small(a, c->stream);
+        const size_t wsb = qgemm_small_workspace(a);
+        void* ws = wsb ? ensure_workspace(c, wsb) : nullptr;
+        if (wsb && !ws) return fail(LUX_BACKEND_ERROR_OUT_OF_MEMORY, "qmatmul: workspace allocation failed");
+        he = launch_qgemm_small(a, ws, c->stream);
     } else {
         return fail(LUX_BACKEND_ERROR_NOT_SUPPORTED, "qmatmul: no kernel for this descriptor");
     }

@@ -6,8 +6,10 @@
 // bf16 output -- a dense contraction (2,216 flop per HBM byte), so the roofline
 // is the fp16/bf16 MFMA peak.
 //
-// Numerics: X (bf16) is staged as fp16, which is exact for 2^-14 <= |x| <= 65504
-// (bf16 carries 8 significant bits, fp16 11).  The dequantised weight q*s is
+// Numerics: X (bf16) is staged as fp16 after dividing each row by a power of two
+// that puts its largest |x| in [2^14, 2^15); bf16 carries 8 significant bits and fp16
+// 11, so the staging is exact for every element within 2^-28 of the row maximum and
+// cannot overflow.  The epilogue multiplies the row back (exact).  The dequantised weight q*s is
 // staged as fp16 rounded to nearest-even: the exact product needs up to 14
 // significant bits, so each staged weight carries a relative error <= 2^-11.
 // Products are exact in the MFMA and accumulate in fp32.  Against the
@@ -76,37 +78,80 @@ __device__ __forceinline__ u32x4 dequant8_f32(uint32_t w, float s) {
 
 // X -> fp16 in staging order.  Runs once per call ahead of the GEMM, so each
 // activation is converted once instead of once per n tile (56 times on config 4).
-// Groups of 8 along k are reordered (k, k+4, k+1, k+5, ...), the order in which
-// dequant8 emits weights; both MFMA operands then agree element by element.
+// Pre-pass, one wave per activation row: X -> fp16 in the staging order (groups of 8
+// along k reordered (k, k+4, k+1, k+5, ...), the order in which dequant8 emits
+// weights, so both MFMA operands agree element by element).  bf16 rows are first
+// divided by their power-of-two factor fac[m] (row_pow2_factor), which the GEMM
+// epilogue multiplies back; fp16 rows are copied as they are (fac = 1).  The first
+// XR * 64 chunks of 8 stay in registers between the max and the conversion.
+constexpr int XR = 8;
+
+__device__ __forceinline__ uint32_t bf16x2_absmax(uint32_t w) {
+    return max(w & 0x7FFFu, (w >> 16) & 0x7FFFu);
+}
+
+__device__ __forceinline__ u32x4 bf16x8_to_staged_f16(u32x4 v, float inv) {
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+    f16 h[8];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        h[2 * q] = (f16)(__builtin_bit_cast(float, w[q] << 16) * inv);
+        h[2 * q + 1] = (f16)(__builtin_bit_cast(float, w[q] & 0xFFFF0000u) * inv);
+    }
+    return u32x4{pack_h2(h[0], h[4]), pack_h2(h[1], h[5]), pack_h2(h[2], h[6]), pack_h2(h[3], h[7])};
+}
+
 template <XKind XK>
-__global__ __launch_bounds__(256) void k_x_to_f16_staged(const void* __restrict__ X,
-                                                         u32x4* __restrict__ out, size_t n8) {
-    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n8; i += (size_t)gridDim.x * 256) {
-        const u32x4 v = reinterpret_cast<const u32x4*>(X)[i];
-        f16 h[8];
-        if constexpr (XK == XKind::BF16) {
-            const uint32_t w[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                h[2 * q] = (f16)__builtin_bit_cast(float, w[q] << 16);
-                h[2 * q + 1] = (f16)__builtin_bit_cast(float, w[q] & 0xFFFF0000u);
-            }
-        } else {
-            const f16x8 f = __builtin_bit_cast(f16x8, v);
-#pragma unroll
-            for (int q = 0; q < 8; ++q) h[q] = f[q];
+__global__ __launch_bounds__(256) void k_x_to_f16_rows(const void* __restrict__ X,
+                                                       u32x4* __restrict__ out,
+                                                       float* __restrict__ fac, int M, int K) {
+    const int lane = threadIdx.x & 63;
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= M) return;
+    const int n8 = K / 8;
+    const u32x4* xr = reinterpret_cast<const u32x4*>(X) + (size_t)row * n8;
+    u32x4* orow = out + (size_t)row * n8;
+    if constexpr (XK == XKind::F16) {
+        for (int c = lane; c < n8; c += 64) {
+            const f16x8 fv = __builtin_bit_cast(f16x8, xr[c]);
+            orow[c] = u32x4{pack_h2(fv[0], fv[4]), pack_h2(fv[1], fv[5]), pack_h2(fv[2], fv[6]),
+                            pack_h2(fv[3], fv[7])};
         }
-        out[i] = u32x4{pack_h2(h[0], h[4]), pack_h2(h[1], h[5]), pack_h2(h[2], h[6]),
-                       pack_h2(h[3], h[7])};
+        if (lane == 0) fac[row] = 1.0f;
+    } else {
+        u32x4 v[XR];
+        uint32_t mx = 0;
+#pragma unroll
+        for (int i = 0; i < XR; ++i) {
+            const int c = lane + 64 * i;
+            v[i] = c < n8 ? xr[c] : u32x4{0u, 0u, 0u, 0u};
+            mx = max(mx, max(max(bf16x2_absmax(v[i].x), bf16x2_absmax(v[i].y)),
+                             max(bf16x2_absmax(v[i].z), bf16x2_absmax(v[i].w))));
+        }
+        for (int c = lane + 64 * XR; c < n8; c += 64) {
+            const u32x4 u = xr[c];
+            mx = max(mx, max(max(bf16x2_absmax(u.x), bf16x2_absmax(u.y)), max(bf16x2_absmax(u.z), bf16x2_absmax(u.w))));
+        }
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) mx = max(mx, (uint32_t)__shfl_xor((int)mx, o, 64));
+        const float f = row_pow2_factor(mx, 7);
+        const float inv = 1.0f / f;  // exact: f is a power of two
+#pragma unroll
+        for (int i = 0; i < XR; ++i) {
+            const int c = lane + 64 * i;
+            if (c < n8) orow[c] = bf16x8_to_staged_f16(v[i], inv);
+        }
+        for (int c = lane + 64 * XR; c < n8; c += 64) orow[c] = bf16x8_to_staged_f16(xr[c], inv);
+        if (lane == 0) fac[row] = f;
     }
 }
 
 // GEMM over the staged X (fp16, staging order) and int4 W.
 template <ScaleKind SK, YKind YK>
 __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2)))
-void k_qgemm_i4_large(const f16* __restrict__ X, const uint32_t* __restrict__ W,
-                      const void* __restrict__ S, void* __restrict__ Y, int M, int N, int K,
-                      int gs, uint32_t xor_mask) {
+void k_qgemm_i4_large(const f16* __restrict__ X, const float* __restrict__ xfac,
+                      const uint32_t* __restrict__ W, const void* __restrict__ S, void* __restrict__ Y,
+                      int M, int N, int K, int gs, uint32_t xor_mask) {
     extern __shared__ __attribute__((aligned(16))) f16 lds[];
     f16* xs = lds;                          // [2][BM][LDS_ROW]
     f16* ws = lds + 2 * BM * LDS_ROW;       // [2][BN][LDS_ROW]
@@ -238,6 +283,12 @@ void k_qgemm_i4_large(const f16* __restrict__ X, const uint32_t* __restrict__ W,
     }
     if (nstages & 1) compute(0, R1);
 
+    // The block's 256 row factors of X (fp32) go to the now idle LDS, once.
+    __syncthreads();
+    float* fac = reinterpret_cast<float*>(lds);
+    if (tid < BM) fac[tid] = m0 + tid < M ? xfac[m0 + tid] : 0.0f;
+    __syncthreads();
+
     // Epilogue: D[i][j] of a 32x32 tile sits in lane j + 32 * ((i / 4) & 1), register
     // 4 * (i / 8) + i % 4.
 #pragma unroll
@@ -247,8 +298,9 @@ void k_qgemm_i4_large(const f16* __restrict__ X, const uint32_t* __restrict__ W,
             const int n = n0 + wn * 64 + 32 * j + (lane & 31);
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-                const int m = m0 + wm * 128 + 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-                if (m < M && n < N) store_y<YK>(Y, (size_t)m * N + n, acc[i][j][r]);
+                const int ml = wm * 128 + 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                const int m = m0 + ml;
+                if (m < M && n < N) store_y<YK>(Y, (size_t)m * N + n, acc[i][j][r] * fac[ml]);
             }
         }
 }
@@ -263,7 +315,7 @@ bool qgemm_i4_large_supported(const QArgs& a) {
 }
 
 template <ScaleKind SK, YKind YK>
-static void launch_t(const QArgs& a, const f16* xst, hipStream_t s) {
+static void launch_t(const QArgs& a, const f16* xst, const float* xfac, hipStream_t s) {
     const dim3 grid((a.n_out + BN - 1) / BN, (a.m + BM - 1) / BM), block(NT);
     const size_t lds = (size_t)2 * (BM + BN) * LDS_ROW * sizeof(f16);
     static bool attr = [] {
@@ -272,37 +324,41 @@ static void launch_t(const QArgs& a, const f16* xst, hipStream_t s) {
         return true;
     }();
     (void)attr;
-    hipLaunchKernelGGL((k_qgemm_i4_large<SK, YK>), grid, block, lds, s, xst,
+    hipLaunchKernelGGL((k_qgemm_i4_large<SK, YK>), grid, block, lds, s, xst, xfac,
                        reinterpret_cast<const uint32_t*>(a.w), a.s, a.y, a.m, a.n_out, a.k,
                        a.group_size, a.xor_mask);
 }
 
 template <ScaleKind SK>
-static bool launch_y(const QArgs& a, const f16* xst, hipStream_t s) {
+static bool launch_y(const QArgs& a, const f16* xst, const float* xfac, hipStream_t s) {
     switch (a.y_kind) {
-        case YKind::F32: launch_t<SK, YKind::F32>(a, xst, s); return true;
-        case YKind::F16: launch_t<SK, YKind::F16>(a, xst, s); return true;
-        case YKind::BF16: launch_t<SK, YKind::BF16>(a, xst, s); return true;
+        case YKind::F32: launch_t<SK, YKind::F32>(a, xst, xfac, s); return true;
+        case YKind::F16: launch_t<SK, YKind::F16>(a, xst, xfac, s); return true;
+        case YKind::BF16: launch_t<SK, YKind::BF16>(a, xst, xfac, s); return true;
         default: return false;
     }
 }
 
-size_t qgemm_i4_large_workspace(const QArgs& a) { return (size_t)a.m * a.k * sizeof(f16); }
+size_t qgemm_i4_large_workspace(const QArgs& a) {
+    // staged X (fp16) followed by the per-row factors (fp32); k % 64 keeps both aligned
+    return (size_t)a.m * a.k * sizeof(f16) + (size_t)a.m * sizeof(float);
+}
 
 hipError_t launch_qgemm_i4_large(const QArgs& a, void* workspace, hipStream_t s) {
-    const size_t n8 = (size_t)a.m * a.k / 8;
-    const unsigned blocks = (unsigned)std::min<size_t>((n8 + 255) / 256, 4096);
     u32x4* xst = reinterpret_cast<u32x4*>(workspace);
+    float* xfac = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + (size_t)a.m * a.k * sizeof(f16));
     if (a.x_kind == XKind::BF16)
-        hipLaunchKernelGGL(k_x_to_f16_staged<XKind::BF16>, dim3(blocks), dim3(256), 0, s, a.x, xst, n8);
+        hipLaunchKernelGGL(k_x_to_f16_rows<XKind::BF16>, dim3((a.m + 3) / 4), dim3(256), 0, s, a.x, xst, xfac,
+                           a.m, a.k);
     else
-        hipLaunchKernelGGL(k_x_to_f16_staged<XKind::F16>, dim3(blocks), dim3(256), 0, s, a.x, xst, n8);
+        hipLaunchKernelGGL(k_x_to_f16_rows<XKind::F16>, dim3((a.m + 3) / 4), dim3(256), 0, s, a.x, xst, xfac,
+                           a.m, a.k);
     const f16* xh = reinterpret_cast<const f16*>(workspace);
     bool ok = false;
     switch (a.scale_kind) {
-        case ScaleKind::F16: ok = launch_y<ScaleKind::F16>(a, xh, s); break;
-        case ScaleKind::F32: ok = launch_y<ScaleKind::F32>(a, xh, s); break;
-        case ScaleKind::GroupScale: ok = launch_y<ScaleKind::GroupScale>(a, xh, s); break;
+        case ScaleKind::F16: ok = launch_y<ScaleKind::F16>(a, xh, xfac, s); break;
+        case ScaleKind::F32: ok = launch_y<ScaleKind::F32>(a, xh, xfac, s); break;
+        case ScaleKind::GroupScale: ok = launch_y<ScaleKind::GroupScale>(a, xh, xfac, s); break;
         default: break;
     }
     if (!ok) return hipErrorInvalidValue;

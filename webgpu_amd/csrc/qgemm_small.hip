@@ -75,7 +75,7 @@ __device__ __forceinline__ f16x8 i4x8_to_f16(uint32_t w, f16x2 s2, uint32_t magi
 template <int WB, int MT, bool PERROW, ScaleKind SK, XKind XK, YKind YK>
 __global__ __launch_bounds__(64 * MAXW) void k_qgemm_small(
     const uint8_t* __restrict__ W, const void* __restrict__ S, const void* __restrict__ X,
-    void* __restrict__ Y, int M, int N, int K, int gs, uint32_t xor_mask) {
+    void* __restrict__ Y, int M, int N, int K, int gs, uint32_t xor_mask, const float* __restrict__ xfac) {
     __shared__ __attribute__((aligned(16))) f16 xs[2][16 * MT][XROW];
 
     const int nw = blockDim.x >> 6;
@@ -93,8 +93,10 @@ __global__ __launch_bounds__(64 * MAXW) void k_qgemm_small(
             const int row = c / (KC / 8), kc = (c % (KC / 8)) * 8;
             f16 h[8];
             if (row < M) {
+                // bf16 / fp32 rows are divided by their power-of-two factor (exact)
+                const float inv = XK == XKind::F16 ? 1.0f : 1.0f / xfac[row];
 #pragma unroll
-                for (int e = 0; e < 8; ++e) h[e] = (f16)load_x<XK>(X, (size_t)row * K + k0 + kc + e);
+                for (int e = 0; e < 8; ++e) h[e] = (f16)(load_x<XK>(X, (size_t)row * K + k0 + kc + e) * inv);
             } else {
 #pragma unroll
                 for (int e = 0; e < 8; ++e) h[e] = (f16)0.0f;
@@ -213,6 +215,7 @@ __global__ __launch_bounds__(64 * MAXW) void k_qgemm_small(
             if (n >= N) continue;
             float v = acc[t][r];
             if constexpr (WB == 8 && PERROW) v *= load_scale_t<SK>(S, (size_t)n);
+            if constexpr (XK != XKind::F16) v *= xfac[m];
             store_y<YK>(Y, (size_t)m * N + n, v);
         }
     }
@@ -229,7 +232,7 @@ bool qgemm_small_supported(const QArgs& a) {
 }
 
 template <int WB, int MT, bool PERROW, ScaleKind SK, XKind XK, YKind YK>
-static void launch_one(const QArgs& a, const void* x, void* y, int m, hipStream_t s) {
+static void launch_one(const QArgs& a, const void* x, void* y, const float* xfac, int m, hipStream_t s) {
     // Waves per block: the largest count <= 16 that divides the 16-row tiles evenly over
     // the CUs (one block per CU), else 4.
     static int cus = 0;
@@ -245,7 +248,7 @@ static void launch_one(const QArgs& a, const void* x, void* y, int m, hipStream_
     const dim3 grid((tiles + nw - 1) / nw), block(64 * nw);
     hipLaunchKernelGGL((k_qgemm_small<WB, MT, PERROW, SK, XK, YK>), grid, block, 0, s,
                        reinterpret_cast<const uint8_t*>(a.w), a.s, x, y, m, a.n_out, a.k,
-                       a.group_size, a.xor_mask);
+                       a.group_size, a.xor_mask, xfac);
 }
 
 template <int WB, bool PERROW, ScaleKind SK, XKind XK, YKind YK>
@@ -257,10 +260,11 @@ static void launch_m(const QArgs& a, hipStream_t s) {
         const int m = std::min(64, a.m - m0);
         const void* x = reinterpret_cast<const uint8_t*>(a.x) + (size_t)m0 * a.k * xel;
         void* y = reinterpret_cast<uint8_t*>(a.y) + (size_t)m0 * a.n_out * yel;
-        if (m <= 16) launch_one<WB, 1, PERROW, SK, XK, YK>(a, x, y, m, s);
-        else if (m <= 32) launch_one<WB, 2, PERROW, SK, XK, YK>(a, x, y, m, s);
-        else if (m <= 48) launch_one<WB, 3, PERROW, SK, XK, YK>(a, x, y, m, s);
-        else launch_one<WB, 4, PERROW, SK, XK, YK>(a, x, y, m, s);
+        const float* xf = a.xfac ? a.xfac + m0 : nullptr;
+        if (m <= 16) launch_one<WB, 1, PERROW, SK, XK, YK>(a, x, y, xf, m, s);
+        else if (m <= 32) launch_one<WB, 2, PERROW, SK, XK, YK>(a, x, y, xf, m, s);
+        else if (m <= 48) launch_one<WB, 3, PERROW, SK, XK, YK>(a, x, y, xf, m, s);
+        else launch_one<WB, 4, PERROW, SK, XK, YK>(a, x, y, xf, m, s);
     }
 }
 
@@ -297,7 +301,39 @@ static bool launch_s(const QArgs& a, hipStream_t s) {
     }
 }
 
-hipError_t launch_qgemm_small(const QArgs& a, hipStream_t s) {
+// Per-row power-of-two factors of bf16 / fp32 activations (row_pow2_factor).
+template <XKind XK>
+__global__ __launch_bounds__(256) void k_row_factors(const void* __restrict__ X, int K,
+                                                     float* __restrict__ fac) {
+    __shared__ uint32_t red[16];
+    const int row = blockIdx.x;
+    uint32_t mx = 0;
+    if constexpr (XK == XKind::F32) {
+        const uint32_t* xr = reinterpret_cast<const uint32_t*>(X) + (size_t)row * K;
+        for (int k = threadIdx.x; k < K; k += 256) mx = max(mx, xr[k] & 0x7FFFFFFFu);
+    } else {
+        const uint16_t* xr = reinterpret_cast<const uint16_t*>(X) + (size_t)row * K;
+        for (int k = threadIdx.x; k < K; k += 256) mx = max(mx, (uint32_t)(xr[k] & 0x7FFFu));
+    }
+    mx = block_max_u32(mx, red);
+    if (threadIdx.x == 0) fac[row] = row_pow2_factor(mx, XK == XKind::F32 ? 23 : 7);
+}
+
+size_t qgemm_small_workspace(const QArgs& a) {
+    return a.x_kind == XKind::F16 ? 0 : (size_t)a.m * sizeof(float);
+}
+
+hipError_t launch_qgemm_small(const QArgs& a0, void* workspace, hipStream_t s) {
+    QArgs a = a0;
+    a.xfac = nullptr;
+    if (a.x_kind == XKind::BF16 || a.x_kind == XKind::F32) {
+        float* fac = static_cast<float*>(workspace);
+        if (a.x_kind == XKind::BF16)
+            hipLaunchKernelGGL(k_row_factors<XKind::BF16>, dim3(a.m), dim3(256), 0, s, a.x, a.k, fac);
+        else
+            hipLaunchKernelGGL(k_row_factors<XKind::F32>, dim3(a.m), dim3(256), 0, s, a.x, a.k, fac);
+        a.xfac = fac;
+    }
     bool ok;
     if (a.wbits == 8) {
         const bool perrow = a.group_size == a.k || a.scale_kind == ScaleKind::None;

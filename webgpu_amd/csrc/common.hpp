@@ -85,6 +85,23 @@ __device__ __forceinline__ void store_y(void* y, size_t idx, float v) {
     else reinterpret_cast<int32_t*>(y)[idx] = (int32_t)v;
 }
 
+// Four consecutive outputs y[idx .. idx+3]; `vec`: one 8- or 16-byte store (the caller
+// guarantees alignment and that all four are in range).  bf16 uses the hardware
+// round-to-nearest-even conversion (v_cvt_pk_bf16_f32).
+typedef __attribute__((ext_vector_type(4))) __bf16 bf16x4;
+template <YKind Y>
+__device__ __forceinline__ void store_y4(void* y, size_t idx, f32x4 v) {
+    if constexpr (Y == YKind::F32) *reinterpret_cast<f32x4*>(static_cast<float*>(y) + idx) = v;
+    else if constexpr (Y == YKind::F16)
+        *reinterpret_cast<f16x4*>(static_cast<f16*>(y) + idx) = __builtin_convertvector(v, f16x4);
+    else if constexpr (Y == YKind::BF16)
+        *reinterpret_cast<bf16x4*>(static_cast<uint16_t*>(y) + idx) = __builtin_convertvector(v, bf16x4);
+    else {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) store_y<Y>(y, idx + r, v[r]);
+    }
+}
+
 template <XKind X>
 __device__ __forceinline__ float load_x(const void* x, size_t idx) {
     if constexpr (X == XKind::F32) return reinterpret_cast<const float*>(x)[idx];

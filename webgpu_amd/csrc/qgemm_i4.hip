@@ -151,7 +151,7 @@ template <ScaleKind SK, YKind YK>
 __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void k_qgemm_i4_large(const f16* __restrict__ X, const float* __restrict__ xfac,
                       const uint32_t* __restrict__ W, const void* __restrict__ S, void* __restrict__ Y,
-                      int M, int N, int K, int gs, uint32_t xor_mask) {
+                      int M, int N, int K, int gs, uint32_t xor_mask, int vec_y) {
     extern __shared__ __attribute__((aligned(16))) f16 lds[];
     f16* xs = lds;                          // [2][BM][LDS_ROW]
     f16* ws = lds + 2 * BM * LDS_ROW;       // [2][BN][LDS_ROW]
@@ -220,14 +220,17 @@ void k_qgemm_i4_large(const f16* __restrict__ X, const float* __restrict__ xfac,
         }
     };
 
-    f32x16 acc[4][2];
+    // acc[j][i]: weight rows (n) are the MFMA's A operand and activation rows (m) its B
+    // operand, so each lane ends up holding four consecutive n of one output row m.
+    f32x16 acc[2][4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int j = 0; j < 2; ++j)
 #pragma unroll
-        for (int j = 0; j < 2; ++j) acc[i][j] = f32x16{};
+        for (int i = 0; i < 4; ++i) acc[j][i] = f32x16{};
 
-    // MFMA operand addressing (v_mfma_f32_32x32x16_f16): A row = lane % 32, B column =
-    // lane % 32, both taking k = 8 * (lane / 32) + 0..7 of the 16-k step.
+    // MFMA operand addressing (v_mfma_f32_32x32x16_f16): A row (weights) = lane % 32,
+    // B column (activations) = lane % 32, both taking k = 8 * (lane / 32) + 0..7 of the
+    // 16-k step.
     const int arow = wm * 128 + (lane & 31), brow = wn * 64 + (lane & 31);
     const int kofs = (lane >> 5) * 8;
 
@@ -257,7 +260,7 @@ void k_qgemm_i4_large(const f16* __restrict__ X, const float* __restrict__ xfac,
             for (int i = 0; i < 4; ++i)
 #pragma unroll
                 for (int j = 0; j < 2; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[kk & 1][i], b[kk & 1][j], acc[i][j], 0, 0, 0);
+                    acc[j][i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(b[kk & 1][j], a[kk & 1][i], acc[j][i], 0, 0, 0);
             if (kk == 0) store_stage(nxt, buf ^ 1);
         }
     };
@@ -289,20 +292,32 @@ void k_qgemm_i4_large(const f16* __restrict__ X, const float* __restrict__ xfac,
     if (tid < BM) fac[tid] = m0 + tid < M ? xfac[m0 + tid] : 0.0f;
     __syncthreads();
 
-    // Epilogue: D[i][j] of a 32x32 tile sits in lane j + 32 * ((i / 4) & 1), register
-    // 4 * (i / 8) + i % 4.
+    // Epilogue: D[r][c] of a 32x32 tile (r = weight row, c = activation row) sits in
+    // lane c + 32 * ((r / 4) & 1), register 4 * (r / 8) + r % 4: registers 4g .. 4g+3
+    // of a lane are the four consecutive n = 8 g + 4 (lane / 32) + 0..3 of row m.
+    const bool vec = vec_y != 0;  // N % 4 == 0 and Y aligned
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < 4; ++i) {
+        const int ml = wm * 128 + 32 * i + (lane & 31);
+        const int m = m0 + ml;
+        if (m >= M) continue;
+        const float fm = fac[ml];
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            const int n = n0 + wn * 64 + 32 * j + (lane & 31);
+        for (int j = 0; j < 2; ++j)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int ml = wm * 128 + 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-                const int m = m0 + ml;
-                if (m < M && n < N) store_y<YK>(Y, (size_t)m * N + n, acc[i][j][r] * fac[ml]);
+            for (int g = 0; g < 4; ++g) {
+                const int n = n0 + wn * 64 + 32 * j + 8 * g + 4 * (lane >> 5);
+                const f32x4 v = f32x4{acc[j][i][4 * g], acc[j][i][4 * g + 1], acc[j][i][4 * g + 2],
+                                      acc[j][i][4 * g + 3]} * fm;
+                if (vec && n + 3 < N) {
+                    store_y4<YK>(Y, (size_t)m * N + n, v);
+                } else {
+#pragma unroll
+                    for (int r = 0; r < 4; ++r)
+                        if (n + r < N) store_y<YK>(Y, (size_t)m * N + n + r, v[r]);
+                }
             }
-        }
+    }
 }
 
 bool qgemm_i4_large_supported(const QArgs& a) {
@@ -326,7 +341,8 @@ static void launch_t(const QArgs& a, const f16* xst, const float* xfac, hipStrea
     (void)attr;
     hipLaunchKernelGGL((k_qgemm_i4_large<SK, YK>), grid, block, lds, s, xst, xfac,
                        reinterpret_cast<const uint32_t*>(a.w), a.s, a.y, a.m, a.n_out, a.k,
-                       a.group_size, a.xor_mask);
+                       a.group_size, a.xor_mask,
+                       (a.n_out % 4 == 0 && ((uintptr_t)a.y & 15u) == 0) ? 1 : 0);
 }
 
 template <ScaleKind SK>

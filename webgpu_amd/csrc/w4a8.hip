@@ -65,24 +65,6 @@ __device__ __forceinline__ u32x4 perm16(u32x4 v) {
     return u32x4{a, b, c, d};
 }
 
-template <YKind YK>
-__device__ __forceinline__ void store4(void* Y, size_t idx, f32x4 v, bool vec) {
-    if (vec) {
-        if constexpr (YK == YKind::F32) {
-            *reinterpret_cast<f32x4*>(static_cast<float*>(Y) + idx) = v;
-        } else if constexpr (YK == YKind::F16) {
-            const f16x4 h = {(_Float16)v[0], (_Float16)v[1], (_Float16)v[2], (_Float16)v[3]};
-            *reinterpret_cast<f16x4*>(static_cast<_Float16*>(Y) + idx) = h;
-        } else {
-#pragma unroll
-            for (int r = 0; r < 4; ++r) store_y<YK>(Y, idx + r, v[r]);
-        }
-    } else {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) store_y<YK>(Y, idx + r, v[r]);
-    }
-}
-
 }  // namespace
 
 // MODE 0: full-K int32; 1: per-group int32 partials; 2: scaled fp output.
@@ -297,7 +279,7 @@ __global__ __launch_bounds__(256) void k_w4a8(const uint8_t* __restrict__ W,
                 } else {
                     const f32x4 v = facc[f][t] * asc;
                     if (full) {
-                        store4<YK>(Y, (size_t)m * N + n, v, true);
+                        store_y4<YK>(Y, (size_t)m * N + n, v);
                     } else {
 #pragma unroll
                         for (int r = 0; r < 4; ++r)

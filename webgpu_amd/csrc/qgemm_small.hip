@@ -31,7 +31,7 @@ namespace {
 
 constexpr int KC = 256;            // k per staged X chunk
 constexpr int XROW = KC + 8;       // LDS halves per staged X row (pad: conflict-free reads)
-constexpr int MAXW = 16;           // max waves per block
+constexpr int MAXW = 8;            // max waves per block (256 VGPRs per lane)
 
 __device__ __forceinline__ uint32_t pack_h2s(f16 a, f16 b) {
     return __builtin_bit_cast(uint32_t, f16x2{a, b});
@@ -85,21 +85,65 @@ __global__ __launch_bounds__(64 * MAXW) void k_qgemm_small(
     const int G = K / gs;
     const uint32_t magic = 0x64006400u;
 
-    // ---- X staging: 16*MT rows x KC k per chunk; 8 elements per thread step,
-    // reordered into the decode order and converted to fp16.
+    // Per-row power-of-two factors of bf16 / fp32 activations, once per block.
+    __shared__ float sfac[16 * MT];
+    if constexpr (XK != XKind::F16) {
+        if (tid < 16 * MT) sfac[tid] = tid < M ? xfac[tid] : 1.0f;
+        __syncthreads();
+    }
+
+    // ---- X staging: 16*MT rows x KC k per chunk = 512*MT chunks of 8 elements.  A chunk is
+    // loaded as one 16-byte vector (two for fp32) ahead of the chunk's weight loads -- loads
+    // retire in issue order, so data needed at the LDS write must be issued before the
+    // long-latency weight prefetch -- and written to LDS after the chunk's MFMAs, converted
+    // to fp16 and reordered into the decode order.
+    constexpr int XS = 2 * MT;                 // chunks per thread (blocks have >= 4 waves)
+    constexpr int XV = XK == XKind::F32 ? 2 : 1;
     const int xchunks = 16 * MT * (KC / 8);
-    auto stage_x = [&](int buf, int k0) {
-        for (int c = tid; c < xchunks; c += blockDim.x) {
-            const int row = c / (KC / 8), kc = (c % (KC / 8)) * 8;
-            f16 h[8];
-            if (row < M) {
-                // bf16 / fp32 rows are divided by their power-of-two factor (exact)
-                const float inv = XK == XKind::F16 ? 1.0f : 1.0f / xfac[row];
+    u32x4 xr[XS][XV];
+    auto load_xc = [&](int k0) {
 #pragma unroll
-                for (int e = 0; e < 8; ++e) h[e] = (f16)(load_x<XK>(X, (size_t)row * K + k0 + kc + e) * inv);
+        for (int i = 0; i < XS; ++i) {
+            const int c = tid + i * (int)blockDim.x;
+            const int row = c / (KC / 8), kc = (c % (KC / 8)) * 8;
+            if (c < xchunks && row < M) {
+                const size_t e = (size_t)row * K + k0 + kc;
+#pragma unroll
+                for (int v = 0; v < XV; ++v)
+                    xr[i][v] = reinterpret_cast<const u32x4*>(static_cast<const uint8_t*>(X) +
+                                                              e * (XK == XKind::F32 ? 4 : 2))[v];
             } else {
 #pragma unroll
-                for (int e = 0; e < 8; ++e) h[e] = (f16)0.0f;
+                for (int v = 0; v < XV; ++v) xr[i][v] = u32x4{0u, 0u, 0u, 0u};
+            }
+        }
+    };
+    auto store_xc = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < XS; ++i) {
+            const int c = tid + i * (int)blockDim.x;
+            if (c >= xchunks) continue;
+            const int row = c / (KC / 8), kc = (c % (KC / 8)) * 8;
+            f16 h[8];
+            if constexpr (XK == XKind::F16) {
+                const f16x8 f = __builtin_bit_cast(f16x8, xr[i][0]);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) h[e] = f[e];
+            } else if constexpr (XK == XKind::BF16) {
+                // bf16 / fp32 rows are divided by their power-of-two factor (exact)
+                const float inv = 1.0f / sfac[row];
+                const uint32_t w[4] = {xr[i][0].x, xr[i][0].y, xr[i][0].z, xr[i][0].w};
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    h[2 * q] = (f16)(__builtin_bit_cast(float, w[q] << 16) * inv);
+                    h[2 * q + 1] = (f16)(__builtin_bit_cast(float, w[q] & 0xFFFF0000u) * inv);
+                }
+            } else {
+                const float inv = 1.0f / sfac[row];
+                const uint32_t w[8] = {xr[i][0].x, xr[i][0].y, xr[i][0].z, xr[i][0].w,
+                                       xr[i][XV - 1].x, xr[i][XV - 1].y, xr[i][XV - 1].z, xr[i][XV - 1].w};
+#pragma unroll
+                for (int e = 0; e < 8; ++e) h[e] = (f16)(__builtin_bit_cast(float, w[e]) * inv);
             }
             u32x4 v;
             if constexpr (WB == 8)  // (0, 2, 1, 3) inside every 4
@@ -112,9 +156,10 @@ __global__ __launch_bounds__(64 * MAXW) void k_qgemm_small(
 
     // ---- weight stream: lane (row r16, quarter kq) reads 16 B per load.  int8: a load
     // covers 64 k (the quarter's 16 bytes = k 16 kq .. 16 kq + 15); int4: 128 k
-    // (32 nibbles = k 32 kq .. 32 kq + 31).
+    // (32 nibbles = k 32 kq .. 32 kq + 31).  The scales a load needs are fetched with it.
     constexpr int KPL = WB == 8 ? 64 : 128;    // k per load (whole wave)
     constexpr int LPC = KC / KPL;              // loads per X chunk
+    constexpr int SPLD = WB == 8 ? (PERROW ? 0 : 4) : 1;  // scales per load per lane
     const int row = min(n0 + r16, N - 1);
     const size_t rowbytes = (size_t)K * WB / 8;
     const uint8_t* wrow = W + (size_t)row * rowbytes + 16 * kq;
@@ -125,20 +170,29 @@ __global__ __launch_bounds__(64 * MAXW) void k_qgemm_small(
 
     const int nchunks = K / KC;
     u32x4 wq[2][LPC];                          // two chunks of weights in flight
+    uint32_t sq[2][LPC][SPLD > 0 ? SPLD : 1];  // their raw scales
     auto load_w = [&](int slot, int chunk) {
         chunk = min(chunk, nchunks - 1);
 #pragma unroll
-        for (int l = 0; l < LPC; ++l)
+        for (int l = 0; l < LPC; ++l) {
             wq[slot][l] = __builtin_nontemporal_load(
                 reinterpret_cast<const u32x4*>(wrow + (size_t)(chunk * LPC + l) * (KPL * WB / 8)));
+            const int kbase = chunk * KC + l * KPL;
+            if constexpr (WB == 4) {
+                sq[slot][l][0] = load_scale_raw<SK>(S, (size_t)row * G + (kbase + 32 * kq) / gs);
+            } else if constexpr (!PERROW) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    sq[slot][l][r] = load_scale_raw<SK>(S, (size_t)min(n0 + 4 * kq + r, N - 1) * G + kbase / gs);
+            }
+        }
     };
 
     // One chunk: KC k from X buffer `buf` and weight registers `slot` (static).
-    auto chunk = [&](int c, int buf, int slot) {
+    auto chunk = [&](int buf, int slot) {
 #pragma unroll
         for (int l = 0; l < LPC; ++l) {
             const u32x4 q = wq[slot][l];
-            const int kbase = c * KC + l * KPL;   // first k of this load
             if constexpr (WB == 8) {
                 // two k-steps of 32: bytes 0-7 and 8-15 of the lane's 16
 #pragma unroll
@@ -155,19 +209,15 @@ __global__ __launch_bounds__(64 * MAXW) void k_qgemm_small(
                         } else {
                             const f32x4 p = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, f32x4{}, 0, 0, 0);
                             // D rows 4*(lane/16) + r: scales of those rows for this group
-                            const int g = kbase / gs;
 #pragma unroll
-                            for (int r = 0; r < 4; ++r) {
-                                const int nr = min(n0 + 4 * kq + r, N - 1);
-                                acc[t][r] = fmaf(p[r], load_scale_t<SK>(S, (size_t)nr * G + g), acc[t][r]);
-                            }
+                            for (int r = 0; r < 4; ++r)
+                                acc[t][r] = fmaf(p[r], scale_from_raw<SK>(sq[slot][l][r]), acc[t][r]);
                         }
                     }
                 }
             } else {
                 // four k-steps of 32: word w covers k 32 kq + 8 w .. + 7 of this load
-                const int g = (kbase + 32 * kq) / gs;
-                const f16 sc = (f16)load_scale_t<SK>(S, (size_t)row * G + g);
+                const f16 sc = (f16)scale_from_raw<SK>(sq[slot][l][0]);
                 const f16x2 s2 = {sc, sc};
                 const uint32_t words[4] = {q.x, q.y, q.z, q.w};
 #pragma unroll
@@ -184,21 +234,24 @@ __global__ __launch_bounds__(64 * MAXW) void k_qgemm_small(
         }
     };
 
-    // Chunks in pairs so the two weight-register slots are static; weights run two
-    // chunks ahead of use, X one chunk ahead (double-buffered LDS).
+    // Chunks in pairs so the weight-register slots are static; weights run two chunks
+    // ahead of use, X one chunk ahead (registers, then the other LDS buffer).
+    load_xc(0);
     load_w(0, 0);
     load_w(1, 1);
-    stage_x(0, 0);
+    store_xc(0);
     __syncthreads();
     for (int c = 0; c < nchunks; c += 2) {
-        if (c + 1 < nchunks) stage_x(1, (c + 1) * KC);
-        chunk(c, 0, 0);
+        if (c + 1 < nchunks) load_xc((c + 1) * KC);
+        chunk(0, 0);
         load_w(0, c + 2);
+        if (c + 1 < nchunks) store_xc(1);
         __syncthreads();
         if (c + 1 < nchunks) {
-            if (c + 2 < nchunks) stage_x(0, (c + 2) * KC);
-            chunk(c + 1, 1, 1);
+            if (c + 2 < nchunks) load_xc((c + 2) * KC);
+            chunk(1, 1);
             load_w(1, c + 3);
+            if (c + 2 < nchunks) store_xc(0);
             __syncthreads();
         }
     }
@@ -233,8 +286,8 @@ bool qgemm_small_supported(const QArgs& a) {
 
 template <int WB, int MT, bool PERROW, ScaleKind SK, XKind XK, YKind YK>
 static void launch_one(const QArgs& a, const void* x, void* y, const float* xfac, int m, hipStream_t s) {
-    // Waves per block: the largest count <= 16 that divides the 16-row tiles evenly over
-    // the CUs (one block per CU), else 4.
+    // Waves per block, 4 .. MAXW: the count that spreads the 16-row tiles evenly over the
+    // CUs (one block per CU) when there is one, else 4.  The X staging assumes >= 4.
     static int cus = 0;
     if (!cus) {
         int dev = 0;
@@ -245,6 +298,7 @@ static void launch_one(const QArgs& a, const void* x, void* y, const float* xfac
     int nw = 4;
     if (tiles % cus == 0 && tiles / cus <= MAXW) nw = tiles / cus;
     else if (tiles <= cus * MAXW && tiles >= cus) nw = (tiles + cus - 1) / cus;
+    nw = std::max(4, std::min(nw, MAXW));
     const dim3 grid((tiles + nw - 1) / nw), block(64 * nw);
     hipLaunchKernelGGL((k_qgemm_small<WB, MT, PERROW, SK, XK, YK>), grid, block, 0, s,
                        reinterpret_cast<const uint8_t*>(a.w), a.s, x, y, m, a.n_out, a.k,

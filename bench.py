@@ -153,7 +153,8 @@ def bench_c1(torch, W, ctx, steps, warmup):
     gbs = C1_BYTES / per / 1e9
     return {"us_per_launch": round(per * 1e6, 2), "value": round(gbs, 2), "unit": "GB/s",
             "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS,
-                         "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None}}
+                         "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
+                         "traffic": measured_traffic("c1")}}
 
 
 def c3_bytes(m):
@@ -182,7 +183,8 @@ def bench_c3(torch, W, ctx, m, steps, warmup):
     gbs = c3_bytes(m) / per / 1e9
     return {"m": m, "us_per_launch": round(per * 1e6, 2), "value": round(gbs, 2), "unit": "GB/s",
             "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS,
-                         "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None}}
+                         "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
+                         "traffic": measured_traffic(f"c3m{m}")}}
 
 
 def bench_c5(torch, W, ctx, steps, warmup):

@@ -138,11 +138,25 @@ __device__ __forceinline__ uint32_t block_max_u32(uint32_t v, uint32_t* red) {
     return r;
 }
 
-// Butterfly sum across the 64 lanes of a wave (every lane gets the total).
+// One DPP step: v + (v as seen through the lane pattern CTRL), rows outside ROWMASK add 0.
+template <int CTRL, int ROWMASK>
+__device__ __forceinline__ float dpp_add(float v) {
+    const int t = __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, ROWMASK, 0xF, false);
+    return v + __builtin_bit_cast(float, t);
+}
+
+// Sum across the 64 lanes of a wave; every lane gets the total.  VALU-only DPP steps
+// (quad_perm xor 1 and xor 2, half-row mirror, row mirror, row_bcast:15 into rows 1/3,
+// row_bcast:31 into rows 2/3) leave the total in lane 63, which is read back as a
+// uniform value: no LDS round trips on the critical path.
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-    return v;
+    v = dpp_add<0xB1, 0xF>(v);
+    v = dpp_add<0x4E, 0xF>(v);
+    v = dpp_add<0x141, 0xF>(v);
+    v = dpp_add<0x140, 0xF>(v);
+    v = dpp_add<0x142, 0xA>(v);
+    v = dpp_add<0x143, 0xC>(v);
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
 }
 #endif
 

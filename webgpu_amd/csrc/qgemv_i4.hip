@@ -15,7 +15,9 @@
 //   - a masked nibble pair is read directly as two fp16 subnormals (n * 2^-24),
 //     v_dot2_f32_f16 accumulates the exact products n*x in fp32, and the offset
 //     of the offset-binary code is removed once per slice as -8 * sum(x);
-//   - each wave owns a run of rows and issues all their loads before any math.
+//   - x is read once per block and shared through LDS;
+//   - each wave owns a run of rows and keeps two rows of loads in flight ahead of
+//     its math; the row sums use a VALU-only DPP wave reduction.
 #include <cstdlib>
 
 #include "common.hpp"
@@ -44,37 +46,39 @@ __device__ __forceinline__ float dot_slice_sub(const uint32_t (&q)[4], const f16
     return fmaf(hi, 0.0625f, lo);
 }
 
-// One wave owns RW consecutive rows (the last wave may own fewer).  It issues every load it will
-// need up front -- x slice, all rows' weight slices, all scales -- and then
-// consumes rows in order, so the math of row r overlaps the loads of rows > r.
-// The host sizes the grid to 8 waves per CU with equal rows per wave.
+// One wave owns RW consecutive rows (the last wave may own fewer) and keeps D rows of
+// weight slices and scales in flight: it issues rows 0..D-1, then for each row r issues
+// row r+D and consumes row r, so the math of row r overlaps the loads of later rows.
+// x is read from HBM/L2 once per block (one 16-byte chunk per thread and SPL pass) and
+// shared through LDS.  The host sizes the grid to 8 waves per CU with equal rows per wave.
 template <int SPL, int RW, int D, ScaleKind SK, YKind YK, bool XOR>
 __global__ __launch_bounds__(256) void k_qgemv_i4_f16(const u32x4* __restrict__ W,
                                                       const void* __restrict__ S,
                                                       const f16* __restrict__ x,
                                                       void* __restrict__ y, int n_out, int K,
-                                                      int spg, uint32_t xor_mask) {
+                                                      int spg_shift, uint32_t xor_mask) {
+    __shared__ u32x4 xs[SPL * 256];  // K <= SPL * 2048 halves
     const int lane = threadIdx.x & 63;
     const int row0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * RW;
-    if (row0 >= n_out) return;
+    const bool active = row0 < n_out;
     const int nrows = min(RW, n_out - row0);
     const int s_row = K >> 5;        // slices per row
-    const int g_row = s_row / spg;   // groups per row
+    const int g_row = s_row >> spg_shift;  // groups per row (slices per group: a power of two)
 
-    // Load order matters: vmcnt retires loads in issue order, so x (an L2 hit)
-    // goes first, then every weight slice and raw scale of the wave's rows.  All
-    // addresses are clamped to valid ones; out-of-range slices get x = 0 after
-    // the loads, and rows past the wave's share are never computed or stored.
-    u32x4 xr[SPL][4];
-    int sl[SPL];
+    // Load order matters: vmcnt retires loads in issue order, so the block's x chunks
+    // (L2 hits) go first, then the first D rows of weight slices and raw scales.  All
+    // addresses are clamped to valid ones; out-of-range slices get x = 0 after the
+    // loads, and rows past the wave's share are never computed or stored.
+    u32x4 xv[SPL];
 #pragma unroll
     for (int j = 0; j < SPL; ++j) {
-        sl[j] = min(lane + 64 * j, s_row - 1);
-        const u32x4* x8 = reinterpret_cast<const u32x4*>(x) + 4 * sl[j];
-#pragma unroll
-        for (int w = 0; w < 4; ++w) xr[j][w] = x8[w];
+        const int c = threadIdx.x + 256 * j;
+        xv[j] = c < K / 8 ? reinterpret_cast<const u32x4*>(x)[c] : u32x4{0u, 0u, 0u, 0u};
     }
     __builtin_amdgcn_sched_barrier(0);  // keep x loads ahead of the weight stream
+    int sl[SPL];
+#pragma unroll
+    for (int j = 0; j < SPL; ++j) sl[j] = min(lane + 64 * j, s_row - 1);
 
     u32x4 q[RW][SPL];
     uint32_t sraw[RW][SPL];
@@ -87,14 +91,21 @@ __global__ __launch_bounds__(256) void k_qgemv_i4_f16(const u32x4* __restrict__ 
         for (int j = 0; j < SPL; ++j) {
             q[r][j] = __builtin_nontemporal_load(W + row * s_row + sl[j]);
             if constexpr (SK == ScaleKind::F16)  // aligned u32 holding this scale (g_row is even)
-                sraw[r][j] = reinterpret_cast<const uint32_t*>(S)[(row * g_row + sl[j] / spg) >> 1];
+                sraw[r][j] = reinterpret_cast<const uint32_t*>(S)[(row * g_row + (sl[j] >> spg_shift)) >> 1];
             else
-                sraw[r][j] = load_scale_raw<SK>(S, row * g_row + sl[j] / spg);
+                sraw[r][j] = load_scale_raw<SK>(S, row * g_row + (sl[j] >> spg_shift));
         }
     };
 #pragma unroll
     for (int r = 0; r < (D < RW ? D : RW); ++r) issue(r);
     __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int j = 0; j < SPL; ++j) {
+        const int c = threadIdx.x + 256 * j;
+        if (c < K / 8) xs[c] = xv[j];
+    }
+    __syncthreads();  // every wave of the block reaches this before any returns
+    if (!active) return;
 
     // x pairs in decode order and, per slice, -8 * sum(x) (offset-binary q = n - 8).
     f16x2 xp[SPL][4][4];
@@ -106,7 +117,7 @@ __global__ __launch_bounds__(256) void k_qgemv_i4_f16(const u32x4* __restrict__ 
         float sx = 0.f;
 #pragma unroll
         for (int w = 0; w < 4; ++w) {
-            const u32x4 u = xr[j][w] & keep;
+            const u32x4 u = xs[4 * sl[j] + w] & keep;
             const f16x8 v = __builtin_bit_cast(f16x8, u);
             xp[j][w][0] = f16x2{v[0], v[4]};
             xp[j][w][1] = f16x2{v[1], v[5]};
@@ -128,7 +139,7 @@ __global__ __launch_bounds__(256) void k_qgemv_i4_f16(const u32x4* __restrict__ 
 #pragma unroll
         for (int j = 0; j < SPL; ++j) {
             uint32_t sb = sraw[r][j];
-            if constexpr (SK == ScaleKind::F16) sb = (sb >> (((sl[j] / spg) & 1) * 16)) & 0xFFFFu;
+            if constexpr (SK == ScaleKind::F16) sb = (sb >> (((sl[j] >> spg_shift) & 1) * 16)) & 0xFFFFu;
             uint32_t qq[4] = {q[r][j].x, q[r][j].y, q[r][j].z, q[r][j].w};
             if constexpr (XOR) {
 #pragma unroll
@@ -190,17 +201,18 @@ static void launch_rwd(const QArgs& a, hipStream_t s) {
     const f16* x = reinterpret_cast<const f16*>(a.x);
     if (a.xor_mask)
         hipLaunchKernelGGL((k_qgemv_i4_f16<SPL, RW, D, SK, YK, true>), grid, block, 0, s, w, a.s, x,
-                           a.y, a.n_out, a.k, a.group_size / 32, a.xor_mask);
+                           a.y, a.n_out, a.k, __builtin_ctz(a.group_size / 32), a.xor_mask);
     else
         hipLaunchKernelGGL((k_qgemv_i4_f16<SPL, RW, D, SK, YK, false>), grid, block, 0, s, w, a.s, x,
-                           a.y, a.n_out, a.k, a.group_size / 32, a.xor_mask);
+                           a.y, a.n_out, a.k, __builtin_ctz(a.group_size / 32), a.xor_mask);
 }
 
-// One row of prefetch (issue row r+1, then compute row r) measured best on MI355X
-// for config 2; deeper prefetch bunches the arrivals and lengthens the tail.
+// Two rows of prefetch (issue row r+2, then compute row r) measured best on MI355X for
+// config 2 (6.9 us against 7.0 us with one row); issuing all rows up front bunches the
+// arrivals and lengthens the tail (8.6 us).
 template <int SPL, int RW, ScaleKind SK, YKind YK>
 static void launch_rw(const QArgs& a, hipStream_t s) {
-    launch_rwd<SPL, RW, 1, SK, YK>(a, s);
+    launch_rwd<SPL, RW, 2, SK, YK>(a, s);
 }
 
 // Rows per wave: enough for 8 waves per CU with equal shares (14336 rows on 256
@@ -268,7 +280,10 @@ static bool launch_generic(const QArgs& a, hipStream_t s) {
 }
 
 hipError_t launch_qgemv_i4(const QArgs& a, hipStream_t s) {
+    // slices per group must be a power of two (the kernel shifts instead of dividing)
+    const int spg = a.group_size / 32;
     const bool fast = a.x_kind == XKind::F16 && a.k % 32 == 0 && a.group_size % 32 == 0 &&
+                      spg > 0 && (spg & (spg - 1)) == 0 &&
                       (a.scale_kind != ScaleKind::F16 || (a.k / a.group_size) % 2 == 0) &&
                       ((uintptr_t)a.w & 15u) == 0 && ((uintptr_t)a.x & 15u) == 0;
     bool launched = false;

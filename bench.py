@@ -58,9 +58,11 @@ def log(msg):
     print(msg, file=sys.stderr, flush=True)
 
 
-def timed_graph(torch, ctx, launch, steps: int, warmup: int):
-    """Warm up eagerly, capture `steps` launches into one graph, replay it once
-    untimed and once timed.  Returns seconds for the timed replay."""
+def timed_graph(torch, ctx, launch, steps: int, warmup: int, settle_s: float = 0.025):
+    """Warm up eagerly (`warmup` launches), capture `steps` launches into one graph,
+    replay it untimed until the GPU has run this workload for `settle_s` seconds (the
+    first replays after a switch of workload run at lower clocks), then time one
+    replay.  Returns seconds for the timed replay."""
     s = torch.cuda.Stream()
     ctx.set_stream(s.cuda_stream)
     ctx.set_synchronous(False)
@@ -71,9 +73,13 @@ def timed_graph(torch, ctx, launch, steps: int, warmup: int):
     with torch.cuda.graph(g, stream=s):
         for i in range(steps):
             launch(i)
-    with torch.cuda.stream(s):
-        g.replay()
-    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(50):
+        with torch.cuda.stream(s):
+            g.replay()
+        torch.cuda.synchronize()
+        if time.perf_counter() - t0 >= settle_s:
+            break
     e0 = torch.cuda.Event(enable_timing=True)
     e1 = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
@@ -94,8 +100,11 @@ def bench_c2(torch, W, ctx, steps, warmup):
     _, Wp, s = int4_weights(r, C2["n_out"], C2["k"], C2["gs"])
     x = r.standard_normal(C2["k"]).astype(np.float16)
     copies = max(2, -(-512 * 2**20 // (Wp.nbytes + s.nbytes)))
-    wbs = [ctx.upload(Wp) for _ in range(copies)]
-    sbs = [ctx.upload(s) for _ in range(copies)]
+    # one weight copy and its scales per "layer", allocated together as a model loader would
+    wbs, sbs = [], []
+    for _ in range(copies):
+        wbs.append(ctx.upload(Wp))
+        sbs.append(ctx.upload(s))
     xb = ctx.upload(x)
     yb = ctx.alloc(C2["n_out"] * 2)
     d = W.qdesc(C2["n_out"], C2["k"], 1, 4, C2["gs"], W.NIBBLE_OFFSET_BINARY, W.SCALE_F16,

@@ -220,6 +220,57 @@ def bench_c5(torch, W, ctx, steps, warmup):
                          "traffic": measured_traffic("c5")}}
 
 
+QW_BYTES = 14336 * 4096 * 4 + 14336 * 4096 // 2 + 14336 * (4096 // 32) * 2  # read f32, write int4 + f16 scales
+
+
+def bench_quantize(torch, W, ctx, steps, warmup):
+    """Producer of configs 2/4: fp32 W [14336 x 4096] -> int4 g32 offset-binary + fp16
+    scales (compute_group_scales + quantize_nax_int4_sym in one pass)."""
+    r = np.random.default_rng(40)
+    x = (r.standard_normal((14336, 4096)) * 0.02).astype(np.float32)
+    copies = 3  # 3 x 235 MB of fp32 input: more than the 256 MB MALL holds
+    xbs = [ctx.upload(x) for _ in range(copies)]
+    qb, sb = ctx.alloc(14336 * 4096 // 2), ctx.alloc(14336 * 128 * 2)
+    d = W.quant_desc(14336, 4096, 4, 32, W.NIBBLE_OFFSET_BINARY, W.SCALE_F16, W.F32)
+
+    def launch(i):
+        ctx.quantize(d, xbs[i % copies], qb, sb)
+
+    n = max(3, min(steps, 30))
+    per = timed_graph(torch, ctx, launch, n, max(1, warmup // 4)) / n
+    for b in xbs:
+        b.free()
+    gbs = QW_BYTES / per / 1e9
+    return {"us_per_launch": round(per * 1e6, 2), "value": round(gbs, 2), "unit": "GB/s",
+            "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS,
+                         "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
+                         "traffic": measured_traffic("quant")}}
+
+
+def bench_c5_fp(torch, W, ctx, steps, warmup):
+    """Config 5 from fp32 activations: per-token int8 quantization (QUANTIZE_X) + W4A8."""
+    from util import int4_weights
+    r = np.random.default_rng(5)
+    _, Wp, s = int4_weights(r, C5["n_out"], C5["k"], C5["gs"], 1)
+    x = r.standard_normal((C5["m"], C5["k"])).astype(np.float32)
+    wb, sb, xb = ctx.upload(Wp), ctx.upload(s), ctx.upload(x)
+    yb = ctx.alloc(C5["m"] * C5["n_out"] * 2)
+    d = W.qdesc(C5["n_out"], C5["k"], C5["m"], 4, C5["gs"], 1, W.SCALE_F16, W.F32, W.F16,
+                W.QFLAG_QUANTIZE_X)
+    ctx.qmatmul(d, wb, sb, xb, None, yb)  # sizes the workspace outside the capture
+
+    def launch(i):
+        ctx.qmatmul(d, wb, sb, xb, None, yb)
+
+    n = max(3, min(steps, 100))
+    per = timed_graph(torch, ctx, launch, n, max(1, warmup // 4)) / n
+    tops = 2 * C5["m"] * C5["n_out"] * C5["k"] / per / 1e12
+    return {"us_per_launch": round(per * 1e6, 2), "value": round(tops, 2), "unit": "TOP/s",
+            "roofline": {"bound": "mfma", "achieved": round(tops, 2), "peak": INT8_MFMA_PEAK_TOPS,
+                         "unit": "TOP/s", "frac": round(tops / INT8_MFMA_PEAK_TOPS, 4),
+                         "traffic": None}}
+
+
 def cpu_baseline_c2(Wp, s, x, budget_s=10.0):
     import oracle
     sf = s.astype(np.float32).reshape(-1)
@@ -245,7 +296,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=10.0)
-    ap.add_argument("--only", choices=["c1", "c2", "c3", "c4", "c5", "copy"], default=None,
+    ap.add_argument("--only", choices=["c1", "c2", "c3", "c4", "c5", "copy", "quant"], default=None,
                     help="run one config only (profiling); the JSON line needs both")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -287,6 +338,10 @@ def main():
         c5 = bench_c5(torch, W, ctx, args.steps, args.warmup)
         log(f"  C5 {c5['us_per_launch']} us/launch, {c5['value']} TOP/s, {c5['hbm_gbs']} GB/s")
         return
+    if args.only == "quant":
+        qz = bench_quantize(torch, W, ctx, args.steps, args.warmup)
+        log(f"  quantize {qz['us_per_launch']} us/launch, {qz['value']} GB/s")
+        return
     log("bench: config 2 int4 GEMV")
     c2 = bench_c2(torch, W, ctx, args.steps, args.warmup)
     log(f"  C2 {c2['per_launch_s']*1e6:.2f} us/launch, {c2['gbs']:.1f} GB/s")
@@ -299,7 +354,7 @@ def main():
         log(f"  C4 {c4['per_launch_s']*1e6:.1f} us/launch, {c4['tflops']:.1f} TFLOP/s")
     except W.LuxError as e:
         log(f"  C4 skipped: {e}")
-    c1, c3s, c5 = None, [], None
+    c1, c3s, c5, c5f, qz = None, [], None, None, None
     try:
         log("bench: config 1 fp32 GEMV through op_matmul_f32")
         c1 = bench_c1(torch, W, ctx, args.steps, args.warmup)
@@ -311,6 +366,12 @@ def main():
         log("bench: config 5 W4A8 M=256")
         c5 = bench_c5(torch, W, ctx, args.steps, args.warmup)
         log(f"  C5 {c5['us_per_launch']} us/launch, {c5['value']} TOP/s")
+        log("bench: config 5 from fp32 activations (per-token quantization + W4A8)")
+        c5f = bench_c5_fp(torch, W, ctx, args.steps, args.warmup)
+        log(f"  C5 fp32-x {c5f['us_per_launch']} us/launch, {c5f['value']} TOP/s")
+        log("bench: int4 g32 quantizer on config-4 weights (fp32 -> int4 + fp16 scales)")
+        qz = bench_quantize(torch, W, ctx, args.steps, args.warmup)
+        log(f"  quantize {qz['us_per_launch']} us/launch, {qz['value']} GB/s")
     except W.LuxError as e:
         log(f"  C1/C3/C5 skipped: {e}")
     cpu = None
@@ -350,6 +411,8 @@ def main():
         "fp32_gemv_c1": c1,
         "int8_gemm_c3": c3s or None,
         "w4a8_gemm_c5": c5,
+        "w4a8_c5_from_fp32_activations": c5f,
+        "quantize_int4_g32_c4_weights": qz,
     }
     print(json.dumps(out), flush=True)
     ctx.close()

@@ -30,7 +30,7 @@
 extern "C" {
 #endif
 
-#define LUX_HIP_QUANT_API_VERSION 1u
+#define LUX_HIP_QUANT_API_VERSION 2u
 
 /* Element types.  The first four keep LuxDtype's numbering (docs/api.md:188-197). */
 typedef enum LuxHipDtype {
@@ -79,6 +79,12 @@ typedef struct LuxHipQMatmulDesc {
 /* W4A8 with y_dtype I32 and group_size < k: write the per-group int32 partial
  * sums P[m][n][g] instead of the full-k sum (checking aid, bit-exact). */
 #define LUX_HIP_QFLAG_GROUP_PARTIALS (1 << 0)
+/* W4A8 from fp activations: x_dtype F32/F16/BF16 is quantized per token to int8 first
+ * (compute_group_scales NAX_INT8_SYM + quantize_nax_int8_group with group_size = k,
+ * quantized_nax.wgsl:157-232,336-362; s = max|row| / 127, q = clamp(round(x / s)))
+ * into the context workspace, then multiplied on the int8 MFMA as with x_dtype I8 and
+ * x_scales = s.  Needs weight_bits 4, group scales, an fp y_dtype and x_scales NULL. */
+#define LUX_HIP_QFLAG_QUANTIZE_X (1 << 1)
 
 /* Quantized matmul / GEMV.  Replaces, by descriptor:
  *   matmul_nax_grouped  quantized_nax.wgsl:568-626  (weight_bits 4, offset-binary,
@@ -96,6 +102,56 @@ LuxBackendError lux_hip_qmatmul(LuxBackendContext* ctx, const LuxHipQMatmulDesc*
                                 LuxBackendBuffer* w, LuxBackendBuffer* w_scales,
                                 LuxBackendBuffer* x, LuxBackendBuffer* x_scales,
                                 LuxBackendBuffer* y);
+
+/* ---- producers and codecs of the matmul inputs ------------------------------ */
+
+/* Descriptor of one symmetric group quantization of X [rows x k] along k. */
+typedef struct LuxHipQuantizeDesc {
+    uint32_t struct_size;   /* sizeof(LuxHipQuantizeDesc)                              */
+    int32_t rows;
+    int32_t k;
+    int32_t weight_bits;    /* 4 or 8                                                  */
+    int32_t group_size;     /* power of two >= 8 dividing k; k gives one scale per row
+                               (per-channel weights, per-token W4A8 activations)      */
+    int32_t nibble_coding;  /* LuxHipNibbleCoding of the int4 output                   */
+    int32_t scale_format;   /* F16, F32 or GROUPSCALE                                  */
+    int32_t x_dtype;        /* F32, F16 or BF16                                        */
+} LuxHipQuantizeDesc;
+
+/* Symmetric group quantizer; replaces compute_group_scales with NAX_INT4_SYM /
+ * NAX_INT8_SYM (quantized_nax.wgsl:157-232) followed by quantize_nax_int4_sym
+ * (:238-262) or quantize_nax_int8_group (:336-362), whose flat groups are the rows'
+ * groups here because group_size divides k:
+ *   s = max(|max x|, |min x|) / (7 for int4, 127 for int8), s == 0 -> 1;
+ *   q = clamp(round_half_even(x / s), -8, 7) or (-128, 127).
+ * q is written in the layout lux_hip_qmatmul reads (int4: 8 per u32 in nibble_coding;
+ * int8: one byte each, [rows x k]); scales [rows x k/group_size] in scale_format
+ * (GROUPSCALE: {s, 0, min x, max x} as the reference writes it).  With SCALE_F16 the
+ * scale is rounded to binary16 first and q is computed with the rounded value, so that
+ * q * s uses the stored scale.  x and q must be 16-byte aligned. */
+LuxBackendError lux_hip_quantize(LuxBackendContext* ctx, const LuxHipQuantizeDesc* desc,
+                                 LuxBackendBuffer* x, LuxBackendBuffer* q, LuxBackendBuffer* scales);
+
+/* Re-code `words` packed int4 words between offset-binary (quantized_nax.wgsl:94-112)
+ * and two's complement (quantized.wgsl:124-156): every nibble xor 8 (ob = tc ^ 0x8), a
+ * copy when the codings agree.  in == out is allowed.  No reference counterpart: the
+ * reference keeps the two codings in separate shader families. */
+LuxBackendError lux_hip_convert_nibbles(LuxBackendContext* ctx, LuxBackendBuffer* in,
+                                        LuxBackendBuffer* out, size_t words, int from_coding,
+                                        int to_coding);
+
+/* Convert `count` group scales between LuxHipScaleFormat F16, F32 and GROUPSCALE (the
+ * 16-byte GroupScale of quantized_nax.wgsl:49-54).  F16 outputs round to nearest even; a
+ * GROUPSCALE written from F16/F32 carries zero_point 0 and group_min = group_max = 0. */
+LuxBackendError lux_hip_convert_scales(LuxBackendContext* ctx, LuxBackendBuffer* in, int in_format,
+                                       LuxBackendBuffer* out, int out_format, size_t count);
+
+/* requantize_int32_to_int8 (quantized.wgsl:560-580, RequantParams {size, input_scale,
+ * output_scale, output_zero_point}): out[i] = clamp(i32(round(f32(in[i]) * input_scale /
+ * output_scale) + output_zero_point), -128, 127), i32 in and out as in the reference. */
+LuxBackendError lux_hip_requantize_i32(LuxBackendContext* ctx, LuxBackendBuffer* in,
+                                       LuxBackendBuffer* out, size_t size, float input_scale,
+                                       float output_scale, int32_t output_zero_point);
 
 /* GemvParams of gemv.wgsl:21-30. */
 typedef struct LuxHipGemvParams {

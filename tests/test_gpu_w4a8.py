@@ -81,3 +81,37 @@ def test_w4a8_rejects(ctx):
         ctx.qmatmul(W.qdesc(32, 128, 4, 4, 64, 1, W.SCALE_F16, W.I8, W.F32), wb, s64, xb,
                     ctx.upload(ascale), yb)
     assert e.value.code == W.LUX_BACKEND_ERROR_NOT_SUPPORTED
+
+
+@pytest.mark.parametrize("xdt", ["f32", "bf16"])
+def test_w4a8_quantize_x(ctx, xdt):
+    """QUANTIZE_X: fp activations quantized per token on the GPU (the W4A8 prologue), then
+    the int8 MFMA.  Bit-identical to feeding the host-quantized int8 activations and their
+    scales (compute_group_scales NAX_INT8_SYM + quantize_nax_int8_group with gs = K), and
+    within tolerance of the oracle's scaled group sums."""
+    from util import bf16_bits, bf16_to_f32
+    r = rng(55)
+    n_out, K, m, gs = 1024, 4096, 256, 128
+    q, Wp, s = int4_weights(r, n_out, K, gs, 1)[0:3]
+    x = r.standard_normal((m, K)).astype(np.float32)
+    if xdt == "bf16":
+        xin = bf16_bits(x)
+        xf = bf16_to_f32(xin)
+        code = W.BF16
+    else:
+        xin, xf, code = x, x, W.F32
+    a8, ascale = quantize_rows_int8(xf)
+    wb, sb = ctx.upload(Wp), ctx.upload(s)
+    y1, y2 = ctx.alloc(m * n_out * 2), ctx.alloc(m * n_out * 2)
+    ctx.qmatmul(W.qdesc(n_out, K, m, 4, gs, 1, W.SCALE_F16, code, W.F16, W.QFLAG_QUANTIZE_X),
+                wb, sb, ctx.upload(xin), None, y1)
+    ctx.qmatmul(W.qdesc(n_out, K, m, 4, gs, 1, W.SCALE_F16, W.I8, W.F16), wb, sb, ctx.upload(a8),
+                ctx.upload(ascale), y2)
+    got = ctx.download(y1, np.float16, (m, n_out))
+    assert np.array_equal(got.view(np.uint16), ctx.download(y2, np.float16, (m, n_out)).view(np.uint16))
+    P = oracle.w4a8_group_partials(Wp, a8, gs, 1).astype(np.float64)
+    ref = (P * s.astype(np.float64)[None, :, :]).sum(axis=2) * ascale.astype(np.float64)[:, None]
+    compare(got.astype(np.float64), round_to(ref.astype(np.float32), "f16"), f"W4A8 QUANTIZE_X {xdt}")
+    with pytest.raises(W.LuxError):  # x_scales must not be passed with QUANTIZE_X
+        ctx.qmatmul(W.qdesc(n_out, K, m, 4, gs, 1, W.SCALE_F16, code, W.F16, W.QFLAG_QUANTIZE_X),
+                    wb, sb, ctx.upload(xin), ctx.upload(ascale), y1)

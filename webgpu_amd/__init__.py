@@ -42,6 +42,7 @@ F32, F16, BF16, I32, I8, I4 = 0, 1, 2, 3, 32, 33
 NIBBLE_OFFSET_BINARY, NIBBLE_TWOS_COMPLEMENT = 0, 1
 SCALE_NONE, SCALE_F16, SCALE_F32, SCALE_GROUPSCALE = 0, 1, 2, 3
 QFLAG_GROUP_PARTIALS = 1
+QFLAG_QUANTIZE_X = 2
 
 
 class LuxError(RuntimeError):
@@ -97,6 +98,12 @@ class QMatmulDesc(Structure):
                 ("flags", c_int32)]
 
 
+class QuantizeDesc(Structure):
+    _fields_ = [("struct_size", c_uint32), ("rows", c_int32), ("k", c_int32),
+                ("weight_bits", c_int32), ("group_size", c_int32), ("nibble_coding", c_int32),
+                ("scale_format", c_int32), ("x_dtype", c_int32)]
+
+
 class GemvParams(Structure):
     _fields_ = [("M", c_uint32), ("N", c_uint32), ("alpha", c_float), ("beta", c_float),
                 ("lda", c_uint32), ("trans", c_uint32), ("_pad0", c_uint32), ("_pad1", c_uint32)]
@@ -119,6 +126,11 @@ EXPORTS = {
     "lux_gpu_backend_init": (c_bool, [POINTER(BackendDesc)]),
     "lux_hip_qmatmul": (c_int, [c_void_p, POINTER(QMatmulDesc), c_void_p, c_void_p, c_void_p,
                                 c_void_p, c_void_p]),
+    "lux_hip_quantize": (c_int, [c_void_p, POINTER(QuantizeDesc), c_void_p, c_void_p, c_void_p]),
+    "lux_hip_convert_nibbles": (c_int, [c_void_p, c_void_p, c_void_p, c_size_t, c_int, c_int]),
+    "lux_hip_convert_scales": (c_int, [c_void_p, c_void_p, c_int, c_void_p, c_int, c_size_t]),
+    "lux_hip_requantize_i32": (c_int, [c_void_p, c_void_p, c_void_p, c_size_t, c_float, c_float,
+                                       c_int32]),
     "lux_hip_gemv_f32": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, POINTER(GemvParams)]),
     "lux_hip_gemv_f16": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_uint32, c_uint32,
                                  c_uint32]),
@@ -330,6 +342,35 @@ class Context:
                                                    scales.handle if scales else None, x.handle,
                                                    x_scales.handle if x_scales else None,
                                                    y.handle), "qmatmul")
+
+    def quantize(self, desc: QuantizeDesc, x: Buffer, q: Buffer, scales: Buffer):
+        self.plugin.check(self.lib.lux_hip_quantize(self.handle, byref(desc), x.handle, q.handle,
+                                                    scales.handle), "quantize")
+
+    def convert_nibbles(self, src: Buffer, dst: Buffer, words: int, from_coding: int,
+                        to_coding: int):
+        self.plugin.check(self.lib.lux_hip_convert_nibbles(self.handle, src.handle, dst.handle,
+                                                           words, from_coding, to_coding),
+                          "convert_nibbles")
+
+    def convert_scales(self, src: Buffer, in_format: int, dst: Buffer, out_format: int,
+                       count: int):
+        self.plugin.check(self.lib.lux_hip_convert_scales(self.handle, src.handle, in_format,
+                                                          dst.handle, out_format, count),
+                          "convert_scales")
+
+    def requantize(self, src: Buffer, dst: Buffer, size: int, input_scale: float,
+                   output_scale: float, output_zero_point: int = 0):
+        self.plugin.check(self.lib.lux_hip_requantize_i32(self.handle, src.handle, dst.handle,
+                                                          size, input_scale, output_scale,
+                                                          output_zero_point), "requantize")
+
+
+def quant_desc(rows: int, k: int, weight_bits: int = 4, group_size: int = 32,
+               nibble_coding: int = NIBBLE_OFFSET_BINARY, scale_format: int = SCALE_F16,
+               x_dtype: int = F32) -> QuantizeDesc:
+    return QuantizeDesc(ctypes.sizeof(QuantizeDesc), rows, k, weight_bits, group_size,
+                        nibble_coding, scale_format, x_dtype)
 
 
 def qdesc(n_out: int, k: int, m: int, weight_bits: int = 4, group_size: int = 32,

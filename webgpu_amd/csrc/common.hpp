@@ -205,4 +205,22 @@ hipError_t launch_qgemm_i4_large(const QArgs& a, void* workspace, hipStream_t s)
 bool w4a8_supported(const QArgs& a);
 hipError_t launch_w4a8(const QArgs& a, hipStream_t s);
 
+// Symmetric group quantizer (scales + packed values) over X [rows x k].
+struct QuantArgs {
+    const void* x;        // [rows x k], x_kind
+    void* q;              // packed int4 (u32 words) or int8
+    void* s;              // scales [rows x k / group_size], scale_kind
+    int rows, k, group_size;  // group_size: a power of two >= 8 dividing k
+    int bits;             // 4 or 8
+    bool offset_binary;   // int4 nibble coding of q
+    ScaleKind scale_kind;
+    XKind x_kind;
+};
+hipError_t launch_quantize(const QuantArgs& a, hipStream_t s);
+// out[i] = in[i] ^ mask over `words` u32 words (nibble re-coding; in == out allowed).
+hipError_t launch_xor_words(const void* in, void* out, size_t words, uint32_t mask, hipStream_t s);
+hipError_t launch_convert_scales(const void* in, ScaleKind ik, void* out, ScaleKind ok, size_t n, hipStream_t s);
+hipError_t launch_requantize(const int32_t* in, int32_t* out, size_t n, float s_in, float s_out, int32_t zp,
+                             hipStream_t s);
+
 }  // namespace luxhip

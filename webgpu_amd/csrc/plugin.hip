@@ -461,7 +461,14 @@ LUX_EXPORT LuxBackendError lux_hip_qmatmul(LuxBackendContext* ctx, const LuxHipQ
     if (d->weight_bits != 4 && d->weight_bits != 8)
         return fail(LUX_BACKEND_ERROR_INVALID_ARGUMENT, "qmatmul: weight_bits must be 4 or 8");
     if (K % 32 != 0) return fail(LUX_BACKEND_ERROR_NOT_SUPPORTED, "qmatmul: k %% 32 != 0");
-    const bool w4a8 = d->x_dtype == LUX_HIP_I8;
+    // QUANTIZE_X: fp activations are quantized per token to int8 first (W4A8 prologue)
+    const bool qx = (d->flags & LUX_HIP_QFLAG_QUANTIZE_X) != 0;
+    if (qx && !(d->weight_bits == 4 && (d->x_dtype == LUX_HIP_F32 || d->x_dtype == LUX_HIP_F16 ||
+                                         d->x_dtype == LUX_HIP_BF16) &&
+                d->y_dtype != LUX_HIP_I32 && d->scale_format != LUX_HIP_SCALE_NONE && !x_scales))
+        return fail(LUX_BACKEND_ERROR_INVALID_ARGUMENT,
+                    "qmatmul: QUANTIZE_X needs int4 weights, fp x and y, group scales and no x_scales");
+    const bool w4a8 = d->x_dtype == LUX_HIP_I8 || qx;
     const bool no_scale = d->scale_format == LUX_HIP_SCALE_NONE;
     if (!no_scale && (gs <= 0 || K % gs != 0 || gs % 8 != 0))
         return fail(LUX_BACKEND_ERROR_INVALID_ARGUMENT, "qmatmul: group_size %d must divide k and be a multiple of 8", gs);
@@ -484,7 +491,7 @@ LUX_EXPORT LuxBackendError lux_hip_qmatmul(LuxBackendContext* ctx, const LuxHipQ
         return fail(LUX_BACKEND_ERROR_INVALID_ARGUMENT, "qmatmul: weight/activation/output buffer too small");
     if (!no_scale && !fits(S, groups * scale_bytes(d->scale_format)))
         return fail(LUX_BACKEND_ERROR_INVALID_ARGUMENT, "qmatmul: scale buffer too small");
-    const bool need_xs = w4a8 && d->y_dtype != LUX_HIP_I32;
+    const bool need_xs = w4a8 && d->y_dtype != LUX_HIP_I32 && !qx;
     if (need_xs && !fits(XS, (size_t)M * 4))
         return fail(LUX_BACKEND_ERROR_INVALID_ARGUMENT, "qmatmul: x_scales (f32 [m]) required for W4A8 fp output");
 
@@ -512,6 +519,28 @@ LUX_EXPORT LuxBackendError lux_hip_qmatmul(LuxBackendContext* ctx, const LuxHipQ
 
     hipError_t he;
     if (w4a8) {
+        if (qx) {  // int8 activations and their f32 per-token scales in the workspace
+            a.x_kind = XKind::I8;
+            uint8_t* ws = static_cast<uint8_t*>(ensure_workspace(c, (size_t)M * K + (size_t)M * 4));
+            if (!ws) return fail(LUX_BACKEND_ERROR_OUT_OF_MEMORY, "qmatmul: workspace allocation failed");
+            a.x = ws;
+            a.xs = reinterpret_cast<const float*>(ws + (size_t)M * K);
+            if (d->weight_bits != 4 || !w4a8_supported(a))
+                return fail(LUX_BACKEND_ERROR_NOT_SUPPORTED, "qmatmul: W4A8 shape/format not supported");
+            QuantArgs qa{};
+            qa.x = X->ptr;
+            qa.q = ws;
+            qa.s = ws + (size_t)M * K;  // k % 32 == 0: 4-byte aligned
+            qa.rows = M;
+            qa.k = K;
+            qa.group_size = K;
+            qa.bits = 8;
+            qa.offset_binary = true;
+            qa.scale_kind = ScaleKind::F32;
+            qa.x_kind = static_cast<XKind>(d->x_dtype);
+            if (hipError_t qe = launch_quantize(qa, c->stream); qe != hipSuccess)
+                return end_op(c, qe, "qmatmul (activation quantization)");
+        }
         if (d->weight_bits != 4 || !w4a8_supported(a))
             return fail(LUX_BACKEND_ERROR_NOT_SUPPORTED, "qmatmul: W4A8 shape/format not supported");
         he = launch_w4a8(a, c->stream);
@@ -536,4 +565,103 @@ LUX_EXPORT LuxBackendError lux_hip_qmatmul(LuxBackendContext* ctx, const LuxHipQ
         return fail(LUX_BACKEND_ERROR_NOT_SUPPORTED, "qmatmul: no kernel for this descriptor");
     }
     return end_op(c, he, "qmatmul");
+}
+
+// ---------------------------------------------------------------- producers / codecs
+// Symmetric group quantizer: compute_group_scales + quantize_nax_int4_sym /
+// quantize_nax_int8_group (quantized_nax.wgsl:157-262,336-362) in one pass.
+LUX_EXPORT LuxBackendError lux_hip_quantize(LuxBackendContext* ctx, const LuxHipQuantizeDesc* d,
+                                            LuxBackendBuffer* x, LuxBackendBuffer* q,
+                                            LuxBackendBuffer* scales) {
+    HipCtx* c = C(ctx);
+    if (!c || !d || !x || !q || !scales) return fail(LUX_BACKEND_ERROR_INVALID_ARGUMENT, "quantize: NULL argument");
+    if (d->struct_size < sizeof(LuxHipQuantizeDesc))
+        return fail(LUX_BACKEND_ERROR_INVALID_ARGUMENT, "quantize: struct_size %u too small", d->struct_size);
+    const int rows = d->rows, K = d->k, gs = d->group_size;
+    if (rows < 0 || K < 0) return fail(LUX_BACKEND_ERROR_INVALID_ARGUMENT, "quantize: negative size");
+    if (d->weight_bits != 4 && d->weight_bits != 8)
+        return fail(LUX_BACKEND_ERROR_INVALID_ARGUMENT, "quantize: weight_bits must be 4 or 8");
+    if (gs < 8 || (gs & (gs - 1)) != 0 || K % gs != 0)
+        return fail(LUX_BACKEND_ERROR_INVALID_ARGUMENT, "quantize: group_size %d must be a power of two >= 8 dividing k", gs);
+    if (d->nibble_coding != LUX_HIP_NIBBLE_OFFSET_BINARY && d->nibble_coding != LUX_HIP_NIBBLE_TWOS_COMPLEMENT)
+        return fail(LUX_BACKEND_ERROR_INVALID_ARGUMENT, "quantize: bad nibble_coding");
+    if (d->x_dtype != LUX_HIP_F32 && d->x_dtype != LUX_HIP_F16 && d->x_dtype != LUX_HIP_BF16)
+        return fail(LUX_BACKEND_ERROR_NOT_SUPPORTED, "quantize: x_dtype must be F32, F16 or BF16");
+    if (scale_bytes(d->scale_format) == 0)
+        return fail(LUX_BACKEND_ERROR_INVALID_ARGUMENT, "quantize: bad scale_format");
+    const size_t n = (size_t)rows * K;
+    HipBuf *X = B(x), *Q = B(q), *S = B(scales);
+    if (!fits(X, n * dtype_bytes(d->x_dtype)) || !fits(Q, n * d->weight_bits / 8) ||
+        !fits(S, (size_t)rows * (K / gs) * scale_bytes(d->scale_format)))
+        return fail(LUX_BACKEND_ERROR_INVALID_ARGUMENT, "quantize: buffer too small");
+    if (((uintptr_t)X->ptr | (uintptr_t)Q->ptr) & 15u)
+        return fail(LUX_BACKEND_ERROR_NOT_SUPPORTED, "quantize: x and q must be 16-byte aligned");
+    if (LuxBackendError e = begin_op(c, "quantize")) return e;
+    if (n == 0) return LUX_BACKEND_OK;
+    QuantArgs a{};
+    a.x = X->ptr;
+    a.q = Q->ptr;
+    a.s = S->ptr;
+    a.rows = rows;
+    a.k = K;
+    a.group_size = gs;
+    a.bits = d->weight_bits;
+    a.offset_binary = d->nibble_coding == LUX_HIP_NIBBLE_OFFSET_BINARY;
+    a.scale_kind = static_cast<ScaleKind>(d->scale_format);
+    a.x_kind = static_cast<XKind>(d->x_dtype);
+    return end_op(c, launch_quantize(a, c->stream), "quantize");
+}
+
+// Nibble re-coding: offset-binary <-> two's complement (each nibble xor 8).
+LUX_EXPORT LuxBackendError lux_hip_convert_nibbles(LuxBackendContext* ctx, LuxBackendBuffer* in,
+                                                   LuxBackendBuffer* out, size_t words, int from_coding,
+                                                   int to_coding) {
+    HipCtx* c = C(ctx);
+    HipBuf *I = B(in), *O = B(out);
+    if (!c || !I || !O) return fail(LUX_BACKEND_ERROR_INVALID_ARGUMENT, "convert_nibbles: NULL argument");
+    auto ok = [](int v) { return v == LUX_HIP_NIBBLE_OFFSET_BINARY || v == LUX_HIP_NIBBLE_TWOS_COMPLEMENT; };
+    if (!ok(from_coding) || !ok(to_coding))
+        return fail(LUX_BACKEND_ERROR_INVALID_ARGUMENT, "convert_nibbles: bad coding");
+    if (!fits(I, words * 4) || !fits(O, words * 4))
+        return fail(LUX_BACKEND_ERROR_INVALID_ARGUMENT, "convert_nibbles: buffer too small");
+    if (((uintptr_t)I->ptr | (uintptr_t)O->ptr) & 3u)
+        return fail(LUX_BACKEND_ERROR_INVALID_ARGUMENT, "convert_nibbles: buffers must be 4-byte aligned");
+    if (LuxBackendError e = begin_op(c, "convert_nibbles")) return e;
+    if (words == 0) return LUX_BACKEND_OK;
+    const uint32_t mask = from_coding == to_coding ? 0u : 0x88888888u;
+    return end_op(c, launch_xor_words(I->ptr, O->ptr, words, mask, c->stream), "convert_nibbles");
+}
+
+// Scale storage conversion between F16, F32 and the 16-byte GroupScale.
+LUX_EXPORT LuxBackendError lux_hip_convert_scales(LuxBackendContext* ctx, LuxBackendBuffer* in, int in_format,
+                                                  LuxBackendBuffer* out, int out_format, size_t count) {
+    HipCtx* c = C(ctx);
+    HipBuf *I = B(in), *O = B(out);
+    if (!c || !I || !O) return fail(LUX_BACKEND_ERROR_INVALID_ARGUMENT, "convert_scales: NULL argument");
+    const size_t ib = scale_bytes(in_format), ob = scale_bytes(out_format);
+    if (!ib || !ob) return fail(LUX_BACKEND_ERROR_INVALID_ARGUMENT, "convert_scales: bad scale format");
+    if (!fits(I, count * ib) || !fits(O, count * ob))
+        return fail(LUX_BACKEND_ERROR_INVALID_ARGUMENT, "convert_scales: buffer too small");
+    if (LuxBackendError e = begin_op(c, "convert_scales")) return e;
+    if (count == 0) return LUX_BACKEND_OK;
+    return end_op(c, launch_convert_scales(I->ptr, static_cast<ScaleKind>(in_format), O->ptr,
+                                           static_cast<ScaleKind>(out_format), count, c->stream),
+                  "convert_scales");
+}
+
+// requantize_int32_to_int8 (quantized.wgsl:560-580): RequantParams {size, input_scale,
+// output_scale, output_zero_point}; i32 in, i32 out clamped to [-128, 127].
+LUX_EXPORT LuxBackendError lux_hip_requantize_i32(LuxBackendContext* ctx, LuxBackendBuffer* in,
+                                                  LuxBackendBuffer* out, size_t size, float input_scale,
+                                                  float output_scale, int32_t output_zero_point) {
+    HipCtx* c = C(ctx);
+    HipBuf *I = B(in), *O = B(out);
+    if (!c || !I || !O) return fail(LUX_BACKEND_ERROR_INVALID_ARGUMENT, "requantize: NULL argument");
+    if (!fits(I, size * 4) || !fits(O, size * 4))
+        return fail(LUX_BACKEND_ERROR_INVALID_ARGUMENT, "requantize: buffer too small");
+    if (LuxBackendError e = begin_op(c, "requantize")) return e;
+    if (size == 0) return LUX_BACKEND_OK;
+    return end_op(c, launch_requantize(static_cast<const int32_t*>(I->ptr), static_cast<int32_t*>(O->ptr), size,
+                                       input_scale, output_scale, output_zero_point, c->stream),
+                  "requantize");
 }

@@ -293,9 +293,9 @@ __global__ __launch_bounds__(256) void k_w4a8(const uint8_t* __restrict__ W,
 
 bool w4a8_supported(const QArgs& a) {
     // groups must hold whole 128-k stages; activations/weights 16-byte aligned
+    if (((uintptr_t)a.w & 15u) != 0 || ((uintptr_t)a.x & 15u) != 0) return false;
     if (a.wbits != 4 || a.x_kind != XKind::I8) return false;
     if (a.k % GK != 0 || a.group_size % GK != 0) return false;
-    if (((uintptr_t)a.w & 15u) != 0 || ((uintptr_t)a.x & 15u) != 0) return false;
     // byte offsets of the buffer loads are 31-bit
     const size_t lim = (size_t)1 << 31;
     if ((size_t)(a.n_out + BR) * a.k / 2 >= lim || (size_t)(a.m + BT) * a.k >= lim) return false;

@@ -103,6 +103,36 @@ LuxBackendError lux_hip_qmatmul(LuxBackendContext* ctx, const LuxHipQMatmulDesc*
                                 LuxBackendBuffer* x, LuxBackendBuffer* x_scales,
                                 LuxBackendBuffer* y);
 
+/* Output epilogues fused into the matmul store, applied in fp32 before the rounding to
+ * y_dtype.  NONE .. ADD_RESIDUAL keep the numbering and formulas of apply_epilogue
+ * (steel_gemm_fused.wgsl:80-127): relu max(0, v); gelu 0.5 v (1 + tanh(0.7978845608
+ * (v + 0.044715 v^3))); silu v / (1 + exp(-v)); tanh; sigmoid 1 / (1 + exp(-v));
+ * v + bias[n] (f32 [n]); v + residual[m, n] (f32 [m x n]).  SILU_MUL is
+ * steel_gemm_silu_mul (:452-558): the weight rows are [gate; up], n_out = 2 N, and
+ * y[m, n] = silu(gate(m, n)) * up(m, n) has N columns. */
+typedef enum LuxHipEpilogue {
+    LUX_HIP_EPILOGUE_NONE = 0,
+    LUX_HIP_EPILOGUE_RELU = 1,
+    LUX_HIP_EPILOGUE_GELU = 2,
+    LUX_HIP_EPILOGUE_SILU = 3,
+    LUX_HIP_EPILOGUE_TANH = 4,
+    LUX_HIP_EPILOGUE_SIGMOID = 5,
+    LUX_HIP_EPILOGUE_ADD_BIAS = 6,
+    LUX_HIP_EPILOGUE_ADD_RESIDUAL = 7,
+    LUX_HIP_EPILOGUE_SILU_MUL = 8
+} LuxHipEpilogue;
+
+/* lux_hip_qmatmul with an output epilogue; replaces steel_gemm_fused
+ * (steel_gemm_fused.wgsl, bias binding 3, residual binding 4, `epilogue` uniform) and
+ * steel_gemm_silu_mul for the weight-only paths (fp activations; NOT_SUPPORTED for
+ * W4A8).  bias / residual are read only for ADD_BIAS / ADD_RESIDUAL (pass NULL
+ * otherwise).  y is [m x N] with N = n_out, or n_out / 2 for SILU_MUL. */
+LuxBackendError lux_hip_qmatmul_ex(LuxBackendContext* ctx, const LuxHipQMatmulDesc* desc,
+                                   LuxBackendBuffer* w, LuxBackendBuffer* w_scales,
+                                   LuxBackendBuffer* x, LuxBackendBuffer* x_scales, int epilogue,
+                                   LuxBackendBuffer* bias, LuxBackendBuffer* residual,
+                                   LuxBackendBuffer* y);
+
 /* ---- producers and codecs of the matmul inputs ------------------------------ */
 
 /* Descriptor of one symmetric group quantization of X [rows x k] along k. */

@@ -55,6 +55,8 @@ _SIGS = {
     "lo_matmul_int4_int8": (None, [_P, _P, _P, _I, _I, _I, _I]),
     "lo_matmul_int8": (None, [_P, _P, _P, _I, _I, _I]),
     "lo_requantize_int32_to_int8": (None, [_P, _P, _SZ, _F, _F, ctypes.c_int32]),
+    "lo_apply_epilogue": (None, [_P, _I, _I, _I, _P, _P]),
+    "lo_silu_mul": (None, [_P, _P, _I, _I]),
     "lo_w4a8_group_partials": (None, [_P, _P, _P, _I, _I, _I, _I, _I]),
     "lo_compute_group_scales": (None, [_P, _SZ, _I, _I, _P, _P, _P, _P]),
     "lo_quantize_nax_int4_sym": (None, [_P, _SZ, _I, _P, _P]),
@@ -325,6 +327,29 @@ def quantize_int8_group(x, gs, scale) -> np.ndarray:
     scale = _c(scale, np.float32)
     out = np.empty((x.size + 3) // 4, np.uint32)
     lib().lo_quantize_nax_int8_group(_p(x.reshape(-1)), x.size, gs, _p(scale), _p(out))
+    return out
+
+
+# --------------------------------------------------------------------------- epilogues
+EPI_NONE, EPI_RELU, EPI_GELU, EPI_SILU, EPI_TANH, EPI_SIGMOID, EPI_ADD_BIAS, EPI_ADD_RESIDUAL = range(8)
+
+
+def apply_epilogue(y, kind, bias=None, residual=None) -> np.ndarray:
+    """apply_epilogue of steel_gemm_fused.wgsl:96-127 on y [m, n] (float32 copy)."""
+    y = np.array(y, np.float32, order="C", copy=True)
+    m, n = y.shape
+    b = _c(bias, np.float32) if bias is not None else np.zeros(1, np.float32)
+    r = _c(residual, np.float32) if residual is not None else np.zeros(1, np.float32)
+    lib().lo_apply_epilogue(_p(y), m, n, int(kind), _p(b), _p(r))
+    return y
+
+
+def silu_mul(gu) -> np.ndarray:
+    """silu(gate) * up for gu [m, 2N] (steel_gemm_fused.wgsl:541-555)."""
+    gu = _c(gu, np.float32)
+    m, n2 = gu.shape
+    out = np.empty((m, n2 // 2), np.float32)
+    lib().lo_silu_mul(_p(gu), _p(out), m, n2 // 2)
     return out
 
 

@@ -542,6 +542,47 @@ void lo_quantize_nax_int8_group(const float* in, size_t size, int gs, const floa
 }
 
 /* ======================================================================= */
+/* GEMM epilogues                                                          */
+/* ======================================================================= */
+
+/* steel_gemm_fused.wgsl:80-93 */
+static float ep_relu(float x) { return fmaxf(0.0f, x); }
+static float ep_gelu(float x) {
+    const float c = 0.7978845608f, a = 0.044715f;
+    return 0.5f * x * (1.0f + tanhf(c * (x + a * x * x * x)));
+}
+static float ep_silu(float x) { return x / (1.0f + expf(-x)); }
+
+/* steel_gemm_fused.wgsl:96-127 */
+void lo_apply_epilogue(float* y, int m, int n, int kind, const float* bias, const float* residual) {
+#pragma omp parallel for schedule(static)
+    for (int r = 0; r < m; ++r)
+        for (int c = 0; c < n; ++c) {
+            const size_t i = (size_t)r * n + c;
+            float v = y[i];
+            switch (kind) {
+                case 1: v = ep_relu(v); break;
+                case 2: v = ep_gelu(v); break;
+                case 3: v = ep_silu(v); break;
+                case 4: v = tanhf(v); break;
+                case 5: v = 1.0f / (1.0f + expf(-v)); break;
+                case 6: v = v + bias[c]; break;
+                case 7: v = v + residual[i]; break;
+                default: break;
+            }
+            y[i] = v;
+        }
+}
+
+/* steel_gemm_fused.wgsl:541-555: silu(gate) * up */
+void lo_silu_mul(const float* gu, float* out, int m, int N) {
+#pragma omp parallel for schedule(static)
+    for (int r = 0; r < m; ++r)
+        for (int c = 0; c < N; ++c)
+            out[(size_t)r * N + c] = ep_silu(gu[(size_t)r * 2 * N + c]) * gu[(size_t)r * 2 * N + N + c];
+}
+
+/* ======================================================================= */
 /* fp64 ground truth                                                       */
 /* ======================================================================= */
 

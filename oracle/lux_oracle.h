@@ -107,6 +107,14 @@ void lo_quantize_nax_int4_sym(const float* in, size_t size, int gs, const float*
 void lo_quantize_nax_int8_group(const float* in, size_t size, int gs, const float* scale,
                                 uint32_t* packed);
 
+/* ---- GEMM epilogues ---------------------------------------------------- */
+/* steel_gemm_fused.wgsl:80-127 apply_epilogue over y [m x n] in place: kind 1 relu,
+ * 2 gelu (tanh form), 3 silu, 4 tanh, 5 sigmoid, 6 + bias[n], 7 + residual[m, n]. */
+void lo_apply_epilogue(float* y, int m, int n, int kind, const float* bias, const float* residual);
+/* steel_gemm_silu_mul (steel_gemm_fused.wgsl:452-558) output stage: out[m, n] =
+ * silu(gu[m, n]) * gu[m, N + n] for gu [m x 2N] (gate columns, then up columns). */
+void lo_silu_mul(const float* gu, float* out, int m, int N);
+
 /* ---- fp64 ground truth ------------------------------------------------ */
 /* y[c, r] = sum_k (q(r,k) * s(r, k/gs)) * x(c, k) in double, token-major x and y.
  * wbits 4 (nibble_coding as above) or 8 (W int8 row-major). */

@@ -282,3 +282,47 @@ def test_group_scales_and_quantizers():
     rng_ = (mxa - mna) / np.float32(15.0)
     rng_ = np.where(rng_ == 0, 1.0, rng_).astype(np.float32)
     assert np.array_equal(sa, rng_)
+
+
+# ------------------------------------------------------------------ GEMM epilogues
+def test_epilogue_activations_pinned():
+    """apply_epilogue (steel_gemm_fused.wgsl:80-127) against library routines and closed
+    forms: relu exact, sigmoid/silu against scipy's expit, tanh against numpy, gelu's tanh
+    form within its known distance of the erf definition, bias/residual exact adds."""
+    from scipy.special import erf, expit
+    x = np.linspace(-12, 12, 4001, dtype=np.float32).reshape(1, -1)
+    xd = x.astype(np.float64)
+    assert np.array_equal(O.apply_epilogue(x, O.EPI_RELU), np.maximum(x, 0))
+    sig = O.apply_epilogue(x, O.EPI_SIGMOID).astype(np.float64)
+    np.testing.assert_allclose(sig, expit(xd), rtol=2e-6, atol=1e-7)
+    assert O.apply_epilogue(np.zeros((1, 1), np.float32), O.EPI_SIGMOID)[0, 0] == 0.5
+    silu = O.apply_epilogue(x, O.EPI_SILU).astype(np.float64)
+    np.testing.assert_allclose(silu, xd * expit(xd), rtol=2e-6, atol=1e-6)
+    th = O.apply_epilogue(x, O.EPI_TANH).astype(np.float64)
+    np.testing.assert_allclose(th, np.tanh(xd), rtol=1e-6, atol=1e-7)
+    gelu = O.apply_epilogue(x, O.EPI_GELU).astype(np.float64)
+    exact = 0.5 * xd * (1 + erf(xd / np.sqrt(2)))
+    assert np.abs(gelu - exact).max() < 1e-3          # tanh approximation of GELU
+    assert np.abs(gelu - exact).max() > 1e-5          # ... and not the erf form itself
+    r = np.random.default_rng(3)
+    y = r.standard_normal((7, 9)).astype(np.float32)
+    b = r.standard_normal(9).astype(np.float32)
+    res = r.standard_normal((7, 9)).astype(np.float32)
+    assert np.array_equal(O.apply_epilogue(y, O.EPI_ADD_BIAS, bias=b), y + b[None, :])
+    assert np.array_equal(O.apply_epilogue(y, O.EPI_ADD_RESIDUAL, residual=res), y + res)
+    assert np.array_equal(O.apply_epilogue(y, O.EPI_NONE), y)
+
+
+def test_silu_mul_pinned():
+    """steel_gemm_silu_mul output stage: gate columns first, up columns second."""
+    from scipy.special import expit
+    r = np.random.default_rng(4)
+    g = r.standard_normal((5, 6)).astype(np.float32)
+    u = r.standard_normal((5, 6)).astype(np.float32)
+    out = O.silu_mul(np.concatenate([g, u], axis=1)).astype(np.float64)
+    gd = g.astype(np.float64)
+    np.testing.assert_allclose(out, gd * expit(gd) * u, rtol=3e-6, atol=1e-7)
+    # halves are not interchangeable: up = 1 gives silu(gate), gate = 0 gives 0
+    assert np.array_equal(O.silu_mul(np.concatenate([g, np.ones_like(g)], 1)),
+                          O.apply_epilogue(g, O.EPI_SILU))
+    assert not O.silu_mul(np.concatenate([np.zeros_like(g), u], 1)).any()

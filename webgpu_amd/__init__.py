@@ -43,6 +43,8 @@ NIBBLE_OFFSET_BINARY, NIBBLE_TWOS_COMPLEMENT = 0, 1
 SCALE_NONE, SCALE_F16, SCALE_F32, SCALE_GROUPSCALE = 0, 1, 2, 3
 QFLAG_GROUP_PARTIALS = 1
 QFLAG_QUANTIZE_X = 2
+(EPI_NONE, EPI_RELU, EPI_GELU, EPI_SILU, EPI_TANH, EPI_SIGMOID, EPI_ADD_BIAS, EPI_ADD_RESIDUAL,
+ EPI_SILU_MUL) = range(9)
 
 
 class LuxError(RuntimeError):
@@ -126,6 +128,8 @@ EXPORTS = {
     "lux_gpu_backend_init": (c_bool, [POINTER(BackendDesc)]),
     "lux_hip_qmatmul": (c_int, [c_void_p, POINTER(QMatmulDesc), c_void_p, c_void_p, c_void_p,
                                 c_void_p, c_void_p]),
+    "lux_hip_qmatmul_ex": (c_int, [c_void_p, POINTER(QMatmulDesc), c_void_p, c_void_p, c_void_p,
+                                   c_void_p, c_int, c_void_p, c_void_p, c_void_p]),
     "lux_hip_quantize": (c_int, [c_void_p, POINTER(QuantizeDesc), c_void_p, c_void_p, c_void_p]),
     "lux_hip_convert_nibbles": (c_int, [c_void_p, c_void_p, c_void_p, c_size_t, c_int, c_int]),
     "lux_hip_convert_scales": (c_int, [c_void_p, c_void_p, c_int, c_void_p, c_int, c_size_t]),
@@ -342,6 +346,14 @@ class Context:
                                                    scales.handle if scales else None, x.handle,
                                                    x_scales.handle if x_scales else None,
                                                    y.handle), "qmatmul")
+
+    def qmatmul_ex(self, desc: QMatmulDesc, w: Buffer, scales: Buffer | None, x: Buffer,
+                   x_scales: Buffer | None, epilogue: int, bias: Buffer | None,
+                   residual: Buffer | None, y: Buffer):
+        self.plugin.check(self.lib.lux_hip_qmatmul_ex(
+            self.handle, byref(desc), w.handle, scales.handle if scales else None, x.handle,
+            x_scales.handle if x_scales else None, epilogue, bias.handle if bias else None,
+            residual.handle if residual else None, y.handle), "qmatmul_ex")
 
     def quantize(self, desc: QuantizeDesc, x: Buffer, q: Buffer, scales: Buffer):
         self.plugin.check(self.lib.lux_hip_quantize(self.handle, byref(desc), x.handle, q.handle,

@@ -28,6 +28,15 @@ struct GroupScale {
 };
 
 enum class ScaleKind : int { None = 0, F16 = 1, F32 = 2, GroupScale = 3 };
+
+// GEMM epilogue kinds: the numbering of apply_epilogue (steel_gemm_fused.wgsl:96-127),
+// plus SiluMul, the gated pair of steel_gemm_silu_mul (:452-558).
+enum class Epi : int { None = 0, Relu = 1, Gelu = 2, Silu = 3, Tanh = 4, Sigmoid = 5, Bias = 6, Residual = 7, SiluMul = 8 };
+struct EpiArgs {
+    int kind;                // Epi
+    const float* bias;       // [n] for Bias
+    const float* residual;   // [m x n] (n = output columns) for Residual
+};
 enum class XKind : int { F32 = 0, F16 = 1, BF16 = 2, I8 = 32 };
 enum class YKind : int { F32 = 0, F16 = 1, BF16 = 2, I32 = 3 };
 
@@ -99,6 +108,24 @@ __device__ __forceinline__ void store_y4(void* y, size_t idx, f32x4 v) {
     else {
 #pragma unroll
         for (int r = 0; r < 4; ++r) store_y<Y>(y, idx + r, v[r]);
+    }
+}
+
+// silu(x) = x / (1 + exp(-x)) (steel_gemm_fused.wgsl:90-93)
+__device__ __forceinline__ float silu_f(float x) { return x / (1.0f + expf(-x)); }
+
+// apply_epilogue (steel_gemm_fused.wgsl:80-127) for output (m, n) of a [M x ny] result;
+// the kind is uniform across the launch, so the switch does not diverge.
+__device__ __forceinline__ float apply_epi(float x, const EpiArgs& e, int m, int n, int ny) {
+    switch (e.kind) {
+        case 1: return fmaxf(0.0f, x);
+        case 2: return 0.5f * x * (1.0f + tanhf(0.7978845608f * (x + 0.044715f * x * x * x)));
+        case 3: return silu_f(x);
+        case 4: return tanhf(x);
+        case 5: return 1.0f / (1.0f + expf(-x));
+        case 6: return x + e.bias[n];
+        case 7: return x + e.residual[(size_t)m * ny + n];
+        default: return x;
     }
 }
 
@@ -179,6 +206,8 @@ struct QArgs {
     XKind x_kind;
     YKind y_kind;
     bool group_partials;  // W4A8: write P[m][n][g]
+    EpiArgs epi;          // output epilogue; SiluMul: n_out = 2 * (output columns),
+                          // weight rows [0, n_out/2) gate and [n_out/2, n_out) up
 };
 
 hipError_t launch_gemv_f32(const float* A, const float* x, float* y, int M, int K, int lda,

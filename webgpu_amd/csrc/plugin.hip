@@ -448,12 +448,16 @@ LUX_EXPORT LuxBackendError lux_hip_gemv_f16(LuxBackendContext* ctx, LuxBackendBu
     return end_op(c, he, "gemv_f16");
 }
 
-LUX_EXPORT LuxBackendError lux_hip_qmatmul(LuxBackendContext* ctx, const LuxHipQMatmulDesc* d,
-                                           LuxBackendBuffer* w, LuxBackendBuffer* w_scales,
-                                           LuxBackendBuffer* x, LuxBackendBuffer* x_scales,
-                                           LuxBackendBuffer* y) {
+namespace {
+LuxBackendError qmatmul_impl(LuxBackendContext* ctx, const LuxHipQMatmulDesc* d, LuxBackendBuffer* w,
+                             LuxBackendBuffer* w_scales, LuxBackendBuffer* x, LuxBackendBuffer* x_scales,
+                             int epilogue, LuxBackendBuffer* bias, LuxBackendBuffer* residual,
+                             LuxBackendBuffer* y) {
     HipCtx* c = C(ctx);
     if (!c || !d || !w || !x || !y) return fail(LUX_BACKEND_ERROR_INVALID_ARGUMENT, "qmatmul: NULL argument");
+    if (epilogue < LUX_HIP_EPILOGUE_NONE || epilogue > LUX_HIP_EPILOGUE_SILU_MUL)
+        return fail(LUX_BACKEND_ERROR_INVALID_ARGUMENT, "qmatmul: bad epilogue %d", epilogue);
+    const bool silu_mul = epilogue == LUX_HIP_EPILOGUE_SILU_MUL;
     if (d->struct_size < sizeof(LuxHipQMatmulDesc))
         return fail(LUX_BACKEND_ERROR_INVALID_ARGUMENT, "qmatmul: struct_size %u too small", d->struct_size);
     const int n_out = d->n_out, K = d->k, M = d->m, gs = d->group_size;
@@ -483,10 +487,20 @@ LUX_EXPORT LuxBackendError lux_hip_qmatmul(LuxBackendContext* ctx, const LuxHipQ
     if (partials && !(w4a8 && d->y_dtype == LUX_HIP_I32 && !no_scale))
         return fail(LUX_BACKEND_ERROR_INVALID_ARGUMENT, "qmatmul: GROUP_PARTIALS needs W4A8, I32 out and a group_size");
 
+    if (epilogue != LUX_HIP_EPILOGUE_NONE && w4a8)
+        return fail(LUX_BACKEND_ERROR_NOT_SUPPORTED, "qmatmul: epilogues are not fused into the W4A8 kernel");
+    if (silu_mul && n_out % 2 != 0)
+        return fail(LUX_BACKEND_ERROR_INVALID_ARGUMENT, "qmatmul: SILU_MUL needs an even n_out (gate rows, then up rows)");
+    const int ny = silu_mul ? n_out / 2 : n_out;  // output columns
     const size_t wn = (size_t)n_out * K * d->weight_bits / 8;
     const size_t groups = no_scale ? 0 : (size_t)n_out * (K / gs);
-    const size_t yn = partials ? (size_t)M * n_out * (K / gs) * 4 : (size_t)M * n_out * yb;
+    const size_t yn = partials ? (size_t)M * n_out * (K / gs) * 4 : (size_t)M * ny * yb;
     HipBuf *W = B(w), *S = B(w_scales), *X = B(x), *XS = B(x_scales), *Y = B(y);
+    HipBuf *BI = B(bias), *RE = B(residual);
+    if (epilogue == LUX_HIP_EPILOGUE_ADD_BIAS && !fits(BI, (size_t)ny * 4))
+        return fail(LUX_BACKEND_ERROR_INVALID_ARGUMENT, "qmatmul: ADD_BIAS needs an f32 bias of n_out elements");
+    if (epilogue == LUX_HIP_EPILOGUE_ADD_RESIDUAL && !fits(RE, (size_t)M * ny * 4))
+        return fail(LUX_BACKEND_ERROR_INVALID_ARGUMENT, "qmatmul: ADD_RESIDUAL needs an f32 residual of m x n_out");
     if (!fits(W, wn) || !fits(X, (size_t)M * K * xb) || !fits(Y, yn))
         return fail(LUX_BACKEND_ERROR_INVALID_ARGUMENT, "qmatmul: weight/activation/output buffer too small");
     if (!no_scale && !fits(S, groups * scale_bytes(d->scale_format)))
@@ -513,6 +527,9 @@ LUX_EXPORT LuxBackendError lux_hip_qmatmul(LuxBackendContext* ctx, const LuxHipQ
     a.x_kind = static_cast<XKind>(d->x_dtype);
     a.y_kind = static_cast<YKind>(d->y_dtype);
     a.group_partials = partials;
+    a.epi.kind = epilogue;
+    a.epi.bias = epilogue == LUX_HIP_EPILOGUE_ADD_BIAS ? static_cast<const float*>(BI->ptr) : nullptr;
+    a.epi.residual = epilogue == LUX_HIP_EPILOGUE_ADD_RESIDUAL ? static_cast<const float*>(RE->ptr) : nullptr;
     // Kernels decode offset-binary nibbles; two's complement becomes offset-binary
     // with one xor per word (ob = tc ^ 0x8, quantized.wgsl:152 vs quantized_nax.wgsl:109).
     a.xor_mask = (d->weight_bits == 4 && d->nibble_coding == LUX_HIP_NIBBLE_TWOS_COMPLEMENT) ? 0x88888888u : 0u;
@@ -544,7 +561,7 @@ LUX_EXPORT LuxBackendError lux_hip_qmatmul(LuxBackendContext* ctx, const LuxHipQ
         if (d->weight_bits != 4 || !w4a8_supported(a))
             return fail(LUX_BACKEND_ERROR_NOT_SUPPORTED, "qmatmul: W4A8 shape/format not supported");
         he = launch_w4a8(a, c->stream);
-    } else if (d->weight_bits == 4 && M == 1) {
+    } else if (d->weight_bits == 4 && M == 1 && !silu_mul) {
         he = launch_qgemv_i4(a, c->stream);
     } else if (M <= 64 && qgemm_small_supported(a)) {
         // decode batches: bandwidth regime, weights streamed once per 64 tokens
@@ -565,6 +582,22 @@ LUX_EXPORT LuxBackendError lux_hip_qmatmul(LuxBackendContext* ctx, const LuxHipQ
         return fail(LUX_BACKEND_ERROR_NOT_SUPPORTED, "qmatmul: no kernel for this descriptor");
     }
     return end_op(c, he, "qmatmul");
+}
+}  // namespace
+
+LUX_EXPORT LuxBackendError lux_hip_qmatmul(LuxBackendContext* ctx, const LuxHipQMatmulDesc* d,
+                                           LuxBackendBuffer* w, LuxBackendBuffer* w_scales,
+                                           LuxBackendBuffer* x, LuxBackendBuffer* x_scales,
+                                           LuxBackendBuffer* y) {
+    return qmatmul_impl(ctx, d, w, w_scales, x, x_scales, LUX_HIP_EPILOGUE_NONE, nullptr, nullptr, y);
+}
+
+LUX_EXPORT LuxBackendError lux_hip_qmatmul_ex(LuxBackendContext* ctx, const LuxHipQMatmulDesc* d,
+                                              LuxBackendBuffer* w, LuxBackendBuffer* w_scales,
+                                              LuxBackendBuffer* x, LuxBackendBuffer* x_scales, int epilogue,
+                                              LuxBackendBuffer* bias, LuxBackendBuffer* residual,
+                                              LuxBackendBuffer* y) {
+    return qmatmul_impl(ctx, d, w, w_scales, x, x_scales, epilogue, bias, residual, y);
 }
 
 // ---------------------------------------------------------------- producers / codecs

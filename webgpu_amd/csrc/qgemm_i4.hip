@@ -151,7 +151,7 @@ template <ScaleKind SK, YKind YK>
 __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void k_qgemm_i4_large(const f16* __restrict__ X, const float* __restrict__ xfac,
                       const uint32_t* __restrict__ W, const void* __restrict__ S, void* __restrict__ Y,
-                      int M, int N, int K, int gs, uint32_t xor_mask, int vec_y) {
+                      int M, int N, int K, int gs, uint32_t xor_mask, int vec_y, EpiArgs epi) {
     extern __shared__ __attribute__((aligned(16))) f16 lds[];
     f16* xs = lds;                          // [2][BM][LDS_ROW]
     f16* ws = lds + 2 * BM * LDS_ROW;       // [2][BN][LDS_ROW]
@@ -180,9 +180,20 @@ void k_qgemm_i4_large(const f16* __restrict__ X, const float* __restrict__ xfac,
         const int m = m0 + xrow + 64 * i;
         xoff[i] = m < M ? (uint32_t)(((size_t)m * K + xk) * 2) : xbytes;
     }
+    // Weight row of LDS row rho.  SiluMul: wave wn's 64 rows are 32 gate rows g0 + 32 wn ..
+    // (its j = 0 block) and the matching up rows nh + g0 + 32 wn .. (j = 1), g0 = 128 *
+    // blockIdx.x, so a gate accumulator and its up accumulator share a lane and register.
+    const bool sm = epi.kind == (int)Epi::SiluMul;
+    const int nh = N / 2, g0 = blockIdx.x * (BN / 2);
+    auto grow = [&](int rho) {  // -1: past the end
+        if (!sm) return n0 + rho < N ? n0 + rho : -1;
+        const int w = rho >> 6, o = rho & 63, g = g0 + 32 * w + (o & 31);
+        return g < nh ? (o < 32 ? g : nh + g) : -1;
+    };
     const int wr_row = tid >> 1, wh = tid & 1;
-    const uint32_t woff = n0 + wr_row < N ? (uint32_t)((size_t)(n0 + wr_row) * (K / 2) + 16 * wh) : wbytes;
-    const int srow = min(n0 + wr_row, N - 1);
+    const int wgr = grow(wr_row);
+    const uint32_t woff = wgr >= 0 ? (uint32_t)((size_t)wgr * (K / 2) + 16 * wh) : wbytes;
+    const int srow = wgr >= 0 ? wgr : N - 1;
     const uint32_t magic = 0x64006400u;
 
     // Staging registers, two sets: the data of stage t is loaded during stage t-2 and
@@ -302,13 +313,34 @@ void k_qgemm_i4_large(const f16* __restrict__ X, const float* __restrict__ xfac,
         const int m = m0 + ml;
         if (m >= M) continue;
         const float fm = fac[ml];
+        if (sm) {  // silu(gate) * up: gate block j = 0, up block j = 1, output [M x nh]
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const int n = g0 + wn * 32 + 8 * g + 4 * (lane >> 5);
+                f32x4 v;
+#pragma unroll
+                for (int r = 0; r < 4; ++r) v[r] = silu_f(acc[0][i][4 * g + r] * fm) * (acc[1][i][4 * g + r] * fm);
+                if (vec && n + 3 < nh) {
+                    store_y4<YK>(Y, (size_t)m * nh + n, v);
+                } else {
+#pragma unroll
+                    for (int r = 0; r < 4; ++r)
+                        if (n + r < nh) store_y<YK>(Y, (size_t)m * nh + n + r, v[r]);
+                }
+            }
+            continue;
+        }
 #pragma unroll
         for (int j = 0; j < 2; ++j)
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
                 const int n = n0 + wn * 64 + 32 * j + 8 * g + 4 * (lane >> 5);
-                const f32x4 v = f32x4{acc[j][i][4 * g], acc[j][i][4 * g + 1], acc[j][i][4 * g + 2],
-                                      acc[j][i][4 * g + 3]} * fm;
+                f32x4 v = f32x4{acc[j][i][4 * g], acc[j][i][4 * g + 1], acc[j][i][4 * g + 2],
+                                acc[j][i][4 * g + 3]} * fm;
+                if (epi.kind != 0) {
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) v[r] = apply_epi(v[r], epi, m, min(n + r, N - 1), N);
+                }
                 if (vec && n + 3 < N) {
                     store_y4<YK>(Y, (size_t)m * N + n, v);
                 } else {
@@ -331,7 +363,9 @@ bool qgemm_i4_large_supported(const QArgs& a) {
 
 template <ScaleKind SK, YKind YK>
 static void launch_t(const QArgs& a, const f16* xst, const float* xfac, hipStream_t s) {
-    const dim3 grid((a.n_out + BN - 1) / BN, (a.m + BM - 1) / BM), block(NT);
+    const bool sm = a.epi.kind == (int)Epi::SiluMul;
+    const int ny = sm ? a.n_out / 2 : a.n_out;  // output columns
+    const dim3 grid(sm ? (ny + BN / 2 - 1) / (BN / 2) : (a.n_out + BN - 1) / BN, (a.m + BM - 1) / BM), block(NT);
     const size_t lds = (size_t)2 * (BM + BN) * LDS_ROW * sizeof(f16);
     static bool attr = [] {
         (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&k_qgemm_i4_large<SK, YK>),
@@ -342,7 +376,7 @@ static void launch_t(const QArgs& a, const f16* xst, const float* xfac, hipStrea
     hipLaunchKernelGGL((k_qgemm_i4_large<SK, YK>), grid, block, lds, s, xst, xfac,
                        reinterpret_cast<const uint32_t*>(a.w), a.s, a.y, a.m, a.n_out, a.k,
                        a.group_size, a.xor_mask,
-                       (a.n_out % 4 == 0 && ((uintptr_t)a.y & 15u) == 0) ? 1 : 0);
+                       (ny % 4 == 0 && ((uintptr_t)a.y & 15u) == 0) ? 1 : 0, a.epi);
 }
 
 template <ScaleKind SK>

@@ -75,12 +75,22 @@ __device__ __forceinline__ f16x8 i4x8_to_f16(uint32_t w, f16x2 s2, uint32_t magi
 template <int WB, int MT, bool PERROW, ScaleKind SK, XKind XK, YKind YK>
 __global__ __launch_bounds__(64 * MAXW) void k_qgemm_small(
     const uint8_t* __restrict__ W, const void* __restrict__ S, const void* __restrict__ X,
-    void* __restrict__ Y, int M, int N, int K, int gs, uint32_t xor_mask, const float* __restrict__ xfac) {
+    void* __restrict__ Y, int M, int N, int K, int gs, uint32_t xor_mask, const float* __restrict__ xfac,
+    EpiArgs epi) {
     __shared__ __attribute__((aligned(16))) f16 xs[2][16 * MT][XROW];
 
     const int nw = blockDim.x >> 6;
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int n0 = (blockIdx.x * nw + wv) * 16;
+    // Weight row of tile row i (0..15).  SiluMul: the tile holds 8 gate rows g0 .. g0+7
+    // (rows 0-7) and the matching up rows nh + g0 .. (rows 8-15), so a gate value and its
+    // up value sit in lanes l and l + 32 of the accumulator.
+    const bool sm = epi.kind == (int)Epi::SiluMul;
+    const int nh = N / 2, g0 = n0 / 2;
+    auto wrow_of = [&](int i) {
+        if (!sm) return min(n0 + i, N - 1);
+        return i < 8 ? min(g0 + i, nh - 1) : nh + min(g0 + i - 8, nh - 1);
+    };
     const int r16 = lane & 15, kq = lane >> 4;
     const int G = K / gs;
     const uint32_t magic = 0x64006400u;
@@ -160,7 +170,7 @@ __global__ __launch_bounds__(64 * MAXW) void k_qgemm_small(
     constexpr int KPL = WB == 8 ? 64 : 128;    // k per load (whole wave)
     constexpr int LPC = KC / KPL;              // loads per X chunk
     constexpr int SPLD = WB == 8 ? (PERROW ? 0 : 4) : 1;  // scales per load per lane
-    const int row = min(n0 + r16, N - 1);
+    const int row = wrow_of(r16);
     const size_t rowbytes = (size_t)K * WB / 8;
     const uint8_t* wrow = W + (size_t)row * rowbytes + 16 * kq;
 
@@ -183,7 +193,7 @@ __global__ __launch_bounds__(64 * MAXW) void k_qgemm_small(
             } else if constexpr (!PERROW) {
 #pragma unroll
                 for (int r = 0; r < 4; ++r)
-                    sq[slot][l][r] = load_scale_raw<SK>(S, (size_t)min(n0 + 4 * kq + r, N - 1) * G + kbase / gs);
+                    sq[slot][l][r] = load_scale_raw<SK>(S, (size_t)wrow_of(4 * kq + r) * G + kbase / gs);
             }
         }
     };
@@ -257,19 +267,24 @@ __global__ __launch_bounds__(64 * MAXW) void k_qgemm_small(
     }
 
     // ---- epilogue: D[i][j] of a 16x16 tile sits in lane j + 16 * (i / 4), register i % 4;
-    // i = weight row (n), j = token (m).
+    // i = weight row (n), j = token (m).  The scalings, then the output epilogue.
 #pragma unroll
     for (int t = 0; t < MT; ++t) {
         const int m = 16 * t + r16;
-        if (m >= M) continue;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            const int n = n0 + 4 * kq + r;
-            if (n >= N) continue;
+            const int i = 4 * kq + r;
             float v = acc[t][r];
-            if constexpr (WB == 8 && PERROW) v *= load_scale_t<SK>(S, (size_t)n);
-            if constexpr (XK != XKind::F16) v *= xfac[m];
-            store_y<YK>(Y, (size_t)m * N + n, v);
+            if constexpr (WB == 8 && PERROW) v *= load_scale_t<SK>(S, (size_t)wrow_of(i));
+            if constexpr (XK != XKind::F16) v *= sfac[m];
+            if (sm) {
+                const float up = __shfl_xor(v, 32, 64);  // tile row i + 8 of the same token
+                const int n = g0 + i;
+                if (kq < 2 && m < M && n < nh) store_y<YK>(Y, (size_t)m * nh + n, silu_f(v) * up);
+            } else {
+                const int n = n0 + i;
+                if (m < M && n < N) store_y<YK>(Y, (size_t)m * N + n, apply_epi(v, epi, m, n, N));
+            }
         }
     }
 }
@@ -285,7 +300,8 @@ bool qgemm_small_supported(const QArgs& a) {
 }
 
 template <int WB, int MT, bool PERROW, ScaleKind SK, XKind XK, YKind YK>
-static void launch_one(const QArgs& a, const void* x, void* y, const float* xfac, int m, hipStream_t s) {
+static void launch_one(const QArgs& a, const void* x, void* y, const float* xfac, int m, EpiArgs epi,
+                       hipStream_t s) {
     // Waves per block, 4 .. MAXW: the count that spreads the 16-row tiles evenly over the
     // CUs (one block per CU) when there is one, else 4.  The X staging assumes >= 4.
     static int cus = 0;
@@ -294,7 +310,8 @@ static void launch_one(const QArgs& a, const void* x, void* y, const float* xfac
         (void)hipGetDevice(&dev);
         if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) cus = 256;
     }
-    const int tiles = (a.n_out + 15) / 16;
+    const bool sm = a.epi.kind == (int)Epi::SiluMul;
+    const int tiles = sm ? (a.n_out / 2 + 7) / 8 : (a.n_out + 15) / 16;
     int nw = 4;
     if (tiles % cus == 0 && tiles / cus <= MAXW) nw = tiles / cus;
     else if (tiles <= cus * MAXW && tiles >= cus) nw = (tiles + cus - 1) / cus;
@@ -302,7 +319,7 @@ static void launch_one(const QArgs& a, const void* x, void* y, const float* xfac
     const dim3 grid((tiles + nw - 1) / nw), block(64 * nw);
     hipLaunchKernelGGL((k_qgemm_small<WB, MT, PERROW, SK, XK, YK>), grid, block, 0, s,
                        reinterpret_cast<const uint8_t*>(a.w), a.s, x, y, m, a.n_out, a.k,
-                       a.group_size, a.xor_mask, xfac);
+                       a.group_size, a.xor_mask, xfac, epi);
 }
 
 template <int WB, bool PERROW, ScaleKind SK, XKind XK, YKind YK>
@@ -310,15 +327,18 @@ static void launch_m(const QArgs& a, hipStream_t s) {
     // m > 64: passes of 64 tokens (each re-reads the weights).
     const size_t xel = a.x_kind == XKind::F32 ? 4 : 2;
     const size_t yel = a.y_kind == YKind::F32 ? 4 : 2;
+    const int ny = a.epi.kind == (int)Epi::SiluMul ? a.n_out / 2 : a.n_out;  // output columns
     for (int m0 = 0; m0 < a.m; m0 += 64) {
         const int m = std::min(64, a.m - m0);
         const void* x = reinterpret_cast<const uint8_t*>(a.x) + (size_t)m0 * a.k * xel;
-        void* y = reinterpret_cast<uint8_t*>(a.y) + (size_t)m0 * a.n_out * yel;
+        void* y = reinterpret_cast<uint8_t*>(a.y) + (size_t)m0 * ny * yel;
         const float* xf = a.xfac ? a.xfac + m0 : nullptr;
-        if (m <= 16) launch_one<WB, 1, PERROW, SK, XK, YK>(a, x, y, xf, m, s);
-        else if (m <= 32) launch_one<WB, 2, PERROW, SK, XK, YK>(a, x, y, xf, m, s);
-        else if (m <= 48) launch_one<WB, 3, PERROW, SK, XK, YK>(a, x, y, xf, m, s);
-        else launch_one<WB, 4, PERROW, SK, XK, YK>(a, x, y, xf, m, s);
+        EpiArgs e = a.epi;
+        if (e.residual) e.residual += (size_t)m0 * ny;
+        if (m <= 16) launch_one<WB, 1, PERROW, SK, XK, YK>(a, x, y, xf, m, e, s);
+        else if (m <= 32) launch_one<WB, 2, PERROW, SK, XK, YK>(a, x, y, xf, m, e, s);
+        else if (m <= 48) launch_one<WB, 3, PERROW, SK, XK, YK>(a, x, y, xf, m, e, s);
+        else launch_one<WB, 4, PERROW, SK, XK, YK>(a, x, y, xf, m, e, s);
     }
 }
 

@@ -56,7 +56,7 @@ __global__ __launch_bounds__(256) void k_qgemv_i4_f16(const u32x4* __restrict__ 
                                                       const void* __restrict__ S,
                                                       const f16* __restrict__ x,
                                                       void* __restrict__ y, int n_out, int K,
-                                                      int spg_shift, uint32_t xor_mask) {
+                                                      int spg_shift, uint32_t xor_mask, EpiArgs epi) {
     __shared__ u32x4 xs[SPL * 256];  // K <= SPL * 2048 halves
     const int lane = threadIdx.x & 63;
     const int row0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * RW;
@@ -152,7 +152,7 @@ __global__ __launch_bounds__(256) void k_qgemv_i4_f16(const u32x4* __restrict__ 
         res = lane == r ? acc : res;
         __builtin_amdgcn_sched_barrier(0);
     }
-    if (lane < nrows) store_y<YK>(y, row0 + lane, res);
+    if (lane < nrows) store_y<YK>(y, row0 + lane, apply_epi(res, epi, 0, row0 + lane, n_out));
 }
 
 // Any activation dtype, any group size that is a multiple of 8: one wave per row,
@@ -162,7 +162,7 @@ __global__ __launch_bounds__(256) void k_qgemv_i4_generic(const uint32_t* __rest
                                                           const void* __restrict__ S,
                                                           ScaleKind sk, const void* __restrict__ x,
                                                           void* __restrict__ y, int n_out, int K,
-                                                          int gs, uint32_t xor_mask) {
+                                                          int gs, uint32_t xor_mask, EpiArgs epi) {
     const int lane = threadIdx.x & 63;
     const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (row >= n_out) return;
@@ -177,7 +177,7 @@ __global__ __launch_bounds__(256) void k_qgemv_i4_generic(const uint32_t* __rest
         acc = fmaf(part, load_scale(S, (size_t)row * g_row + (8 * wi) / gs, sk), acc);
     }
     acc = wave_sum(acc);
-    if (lane == 0) store_y<YK>(y, row, acc);
+    if (lane == 0) store_y<YK>(y, row, apply_epi(acc, epi, 0, row, n_out));
 }
 
 static int device_cus() {
@@ -201,10 +201,10 @@ static void launch_rwd(const QArgs& a, hipStream_t s) {
     const f16* x = reinterpret_cast<const f16*>(a.x);
     if (a.xor_mask)
         hipLaunchKernelGGL((k_qgemv_i4_f16<SPL, RW, D, SK, YK, true>), grid, block, 0, s, w, a.s, x,
-                           a.y, a.n_out, a.k, __builtin_ctz(a.group_size / 32), a.xor_mask);
+                           a.y, a.n_out, a.k, __builtin_ctz(a.group_size / 32), a.xor_mask, a.epi);
     else
         hipLaunchKernelGGL((k_qgemv_i4_f16<SPL, RW, D, SK, YK, false>), grid, block, 0, s, w, a.s, x,
-                           a.y, a.n_out, a.k, __builtin_ctz(a.group_size / 32), a.xor_mask);
+                           a.y, a.n_out, a.k, __builtin_ctz(a.group_size / 32), a.xor_mask, a.epi);
 }
 
 // Two rows of prefetch (issue row r+2, then compute row r) measured best on MI355X for
@@ -265,15 +265,15 @@ static bool launch_generic(const QArgs& a, hipStream_t s) {
     switch (a.y_kind) {
         case YKind::F32:
             hipLaunchKernelGGL((k_qgemv_i4_generic<XK, YKind::F32>), grid, block, 0, s, w, a.s,
-                               a.scale_kind, a.x, a.y, a.n_out, a.k, a.group_size, a.xor_mask);
+                               a.scale_kind, a.x, a.y, a.n_out, a.k, a.group_size, a.xor_mask, a.epi);
             return true;
         case YKind::F16:
             hipLaunchKernelGGL((k_qgemv_i4_generic<XK, YKind::F16>), grid, block, 0, s, w, a.s,
-                               a.scale_kind, a.x, a.y, a.n_out, a.k, a.group_size, a.xor_mask);
+                               a.scale_kind, a.x, a.y, a.n_out, a.k, a.group_size, a.xor_mask, a.epi);
             return true;
         case YKind::BF16:
             hipLaunchKernelGGL((k_qgemv_i4_generic<XK, YKind::BF16>), grid, block, 0, s, w, a.s,
-                               a.scale_kind, a.x, a.y, a.n_out, a.k, a.group_size, a.xor_mask);
+                               a.scale_kind, a.x, a.y, a.n_out, a.k, a.group_size, a.xor_mask, a.epi);
             return true;
         default: return false;
     }

@@ -183,6 +183,28 @@ LuxBackendError lux_hip_requantize_i32(LuxBackendContext* ctx, LuxBackendBuffer*
                                        LuxBackendBuffer* out, size_t size, float input_scale,
                                        float output_scale, int32_t output_zero_point);
 
+/* ---- around the path: RMS normalisation ------------------------------------ */
+
+/* RMSNormParams of rms_norm.wgsl:25-30, plus the element types of input and output
+ * (the WGSL is f32 only; F16/BF16 let the normalised activations feed the quantized
+ * GEMV directly).  gamma and rms_out are f32. */
+typedef struct LuxHipRmsNormParams {
+    uint32_t batch_size;   /* rows                                          */
+    uint32_t hidden_size;  /* elements per row                              */
+    float eps;
+    int32_t x_dtype;       /* F32, F16 or BF16                              */
+    int32_t y_dtype;       /* F32, F16 or BF16                              */
+} LuxHipRmsNormParams;
+
+/* rms_norm (rms_norm.wgsl:50-110): per row, r = 1 / sqrt(sum(x^2) / hidden + eps),
+ * y = x * r * gamma[i], rms_out[row] = r (rms_out may be NULL).  The ABI-v3 slot
+ * op_rms_norm_f32 exists, but the reference leaves it NULL without a signature
+ * (src/webgpu_plugin.cpp:4072), so this is an extra symbol.  The elementwise slots
+ * op_add/sub/mul/div_f32 of the vtable are filled (src/webgpu_plugin.cpp:1637-1719). */
+LuxBackendError lux_hip_rms_norm(LuxBackendContext* ctx, const LuxHipRmsNormParams* params,
+                                 LuxBackendBuffer* input, LuxBackendBuffer* gamma,
+                                 LuxBackendBuffer* output, LuxBackendBuffer* rms_out);
+
 /* GemvParams of gemv.wgsl:21-30. */
 typedef struct LuxHipGemvParams {
     uint32_t M;     /* rows of A                               */

@@ -57,6 +57,7 @@ _SIGS = {
     "lo_requantize_int32_to_int8": (None, [_P, _P, _SZ, _F, _F, ctypes.c_int32]),
     "lo_apply_epilogue": (None, [_P, _I, _I, _I, _P, _P]),
     "lo_silu_mul": (None, [_P, _P, _I, _I]),
+    "lo_rms_norm": (None, [_P, _P, _P, _P, _I, _I, _F]),
     "lo_w4a8_group_partials": (None, [_P, _P, _P, _I, _I, _I, _I, _I]),
     "lo_compute_group_scales": (None, [_P, _SZ, _I, _I, _P, _P, _P, _P]),
     "lo_quantize_nax_int4_sym": (None, [_P, _SZ, _I, _P, _P]),
@@ -351,6 +352,17 @@ def silu_mul(gu) -> np.ndarray:
     out = np.empty((m, n2 // 2), np.float32)
     lib().lo_silu_mul(_p(gu), _p(out), m, n2 // 2)
     return out
+
+
+def rms_norm(x, gamma, eps=1e-6):
+    """rms_norm.wgsl on x [rows, hidden] (float32); returns (y, rms per row)."""
+    x = _c(x, np.float32)
+    rows, hidden = x.shape
+    g = _c(gamma, np.float32)
+    y = np.empty_like(x)
+    r = np.empty(rows, np.float32)
+    lib().lo_rms_norm(_p(x), _p(g), _p(y), _p(r), rows, hidden, float(eps))
+    return y, r
 
 
 # --------------------------------------------------------------------------- ground truth

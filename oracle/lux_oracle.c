@@ -582,6 +582,27 @@ void lo_silu_mul(const float* gu, float* out, int m, int N) {
             out[(size_t)r * N + c] = ep_silu(gu[(size_t)r * 2 * N + c]) * gu[(size_t)r * 2 * N + N + c];
 }
 
+/* rms_norm.wgsl:50-110 */
+void lo_rms_norm(const float* x, const float* gamma, float* y, float* rms_out, int rows, int hidden,
+                 float eps) {
+#pragma omp parallel for schedule(static)
+    for (int r = 0; r < rows; ++r) {
+        const float* xr = x + (size_t)r * hidden;
+        float sh[WG];
+        for (int t = 0; t < WG; ++t) {
+            float s = 0.0f;
+            for (int i = t; i < hidden; i += WG) s += xr[i] * xr[i];
+            sh[t] = s;
+        }
+        for (int stride = WG / 2; stride > 0; stride >>= 1)
+            for (int t = 0; t < stride; ++t) sh[t] += sh[t + stride];
+        const float mean_sq = sh[0] / (float)hidden;
+        const float rms = 1.0f / sqrtf(mean_sq + eps);
+        if (rms_out) rms_out[r] = rms;
+        for (int i = 0; i < hidden; ++i) y[(size_t)r * hidden + i] = xr[i] * rms * gamma[i];
+    }
+}
+
 /* ======================================================================= */
 /* fp64 ground truth                                                       */
 /* ======================================================================= */

@@ -115,6 +115,13 @@ void lo_apply_epilogue(float* y, int m, int n, int kind, const float* bias, cons
  * silu(gu[m, n]) * gu[m, N + n] for gu [m x 2N] (gate columns, then up columns). */
 void lo_silu_mul(const float* gu, float* out, int m, int N);
 
+/* ---- around the path ---------------------------------------------------- */
+/* rms_norm.wgsl:50-110: per row r = 1 / sqrt(sum(x^2) / hidden + eps) with the sum in
+ * the shader's order (256 strided partial sums, then the tree), y = x * r * gamma[i],
+ * rms_out[row] = r (rms_out may be NULL). */
+void lo_rms_norm(const float* x, const float* gamma, float* y, float* rms_out, int rows, int hidden,
+                 float eps);
+
 /* ---- fp64 ground truth ------------------------------------------------ */
 /* y[c, r] = sum_k (q(r,k) * s(r, k/gs)) * x(c, k) in double, token-major x and y.
  * wbits 4 (nibble_coding as above) or 8 (W int8 row-major). */

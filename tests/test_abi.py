@@ -38,7 +38,7 @@ def test_backend_init_descriptor():
     assert filled == {"create_context", "destroy_context", "get_device_count", "get_device_info",
                       "sync", "buffer_alloc", "buffer_alloc_with_data", "buffer_free",
                       "buffer_copy_to_host", "buffer_copy_from_host", "buffer_get_host_ptr",
-                      "op_matmul_f32"}
+                      "op_add_f32", "op_sub_f32", "op_mul_f32", "op_div_f32", "op_matmul_f32"}
     # init(NULL) must fail cleanly
     assert not p.lib.lux_gpu_backend_init(None)
 
@@ -51,6 +51,9 @@ def test_null_arguments_rejected():
         W.LUX_BACKEND_ERROR_INVALID_ARGUMENT
     assert L.lux_hip_gemv_f32(None, None, None, None, None) == W.LUX_BACKEND_ERROR_INVALID_ARGUMENT
     assert p.vt_matmul(None, None, None, None, 4, 4, 4) == W.LUX_BACKEND_ERROR_INVALID_ARGUMENT
+    for op in ("add", "sub", "mul", "div"):
+        assert p.vt_binary[op](None, None, None, None, 4) == W.LUX_BACKEND_ERROR_INVALID_ARGUMENT
+    assert L.lux_hip_rms_norm(None, None, None, None, None, None) == W.LUX_BACKEND_ERROR_INVALID_ARGUMENT
     assert p.vt_count(None) == W.LUX_BACKEND_ERROR_INVALID_ARGUMENT
     assert p.vt_info(None, None) == W.LUX_BACKEND_ERROR_INVALID_ARGUMENT
     assert L.lux_hip_context_set_synchronous(None, 1) == W.LUX_BACKEND_ERROR_INVALID_ARGUMENT

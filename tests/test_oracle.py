@@ -326,3 +326,23 @@ def test_silu_mul_pinned():
     assert np.array_equal(O.silu_mul(np.concatenate([g, np.ones_like(g)], 1)),
                           O.apply_epilogue(g, O.EPI_SILU))
     assert not O.silu_mul(np.concatenate([np.zeros_like(g), u], 1)).any()
+
+
+# ------------------------------------------------------------------ around the path
+def test_rms_norm_pinned():
+    """rms_norm.wgsl restated: against an fp64 evaluation of the definition, and the closed
+    forms of constant rows (r = 1/sqrt(c^2 + eps)) and zero rows (r = 1/sqrt(eps))."""
+    r = np.random.default_rng(12)
+    x = r.standard_normal((5, 3000)).astype(np.float32)
+    g = r.uniform(0.5, 1.5, 3000).astype(np.float32)
+    y, rms = O.rms_norm(x, g, 1e-6)
+    xd = x.astype(np.float64)
+    rd = 1.0 / np.sqrt((xd * xd).mean(axis=1) + 1e-6)
+    np.testing.assert_allclose(rms, rd, rtol=2e-6)
+    np.testing.assert_allclose(y, xd * rd[:, None] * g, rtol=5e-6, atol=1e-7)
+    c = np.full((2, 512), 0.75, np.float32)
+    c[1] = 0.0
+    yc, rc = O.rms_norm(c, np.ones(512, np.float32), 1e-5)
+    assert abs(rc[0] - 1 / np.sqrt(0.5625 + 1e-5)) < 1e-6 * rc[0]
+    assert abs(rc[1] - 1 / np.sqrt(1e-5)) < 1e-6 * rc[1]
+    assert not yc[1].any()

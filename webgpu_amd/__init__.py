@@ -106,6 +106,11 @@ class QuantizeDesc(Structure):
                 ("scale_format", c_int32), ("x_dtype", c_int32)]
 
 
+class RmsNormParams(Structure):
+    _fields_ = [("batch_size", c_uint32), ("hidden_size", c_uint32), ("eps", c_float),
+                ("x_dtype", c_int32), ("y_dtype", c_int32)]
+
+
 class GemvParams(Structure):
     _fields_ = [("M", c_uint32), ("N", c_uint32), ("alpha", c_float), ("beta", c_float),
                 ("lda", c_uint32), ("trans", c_uint32), ("_pad0", c_uint32), ("_pad1", c_uint32)]
@@ -123,6 +128,7 @@ _T_FREE = CFUNCTYPE(None, c_void_p, c_void_p)
 _T_COPY = CFUNCTYPE(c_int, c_void_p, c_void_p, c_void_p, c_size_t)
 _T_HOSTPTR = CFUNCTYPE(c_void_p, c_void_p, c_void_p)
 _T_MATMUL = CFUNCTYPE(c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_int)
+_T_BINARY = CFUNCTYPE(c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_size_t)
 
 EXPORTS = {
     "lux_gpu_backend_init": (c_bool, [POINTER(BackendDesc)]),
@@ -130,6 +136,8 @@ EXPORTS = {
                                 c_void_p, c_void_p]),
     "lux_hip_qmatmul_ex": (c_int, [c_void_p, POINTER(QMatmulDesc), c_void_p, c_void_p, c_void_p,
                                    c_void_p, c_int, c_void_p, c_void_p, c_void_p]),
+    "lux_hip_rms_norm": (c_int, [c_void_p, POINTER(RmsNormParams), c_void_p, c_void_p, c_void_p,
+                                 c_void_p]),
     "lux_hip_quantize": (c_int, [c_void_p, POINTER(QuantizeDesc), c_void_p, c_void_p, c_void_p]),
     "lux_hip_convert_nibbles": (c_int, [c_void_p, c_void_p, c_void_p, c_size_t, c_int, c_int]),
     "lux_hip_convert_scales": (c_int, [c_void_p, c_void_p, c_int, c_void_p, c_int, c_size_t]),
@@ -240,6 +248,7 @@ class Plugin:
         self.vt_from_host = _T_COPY(vt.buffer_copy_from_host)
         self.vt_host_ptr = _T_HOSTPTR(vt.buffer_get_host_ptr)
         self.vt_matmul = _T_MATMUL(vt.op_matmul_f32)
+        self.vt_binary = {op: _T_BINARY(getattr(vt, f"op_{op}_f32")) for op in ("add", "sub", "mul", "div")}
 
     def device_count(self) -> int:
         n = c_int(-1)
@@ -326,6 +335,11 @@ class Context:
         return Buffer(self, h, nbytes, keepalive=tensor)
 
     # -- ops
+    def binary_f32(self, op: str, a: Buffer, b: Buffer, out: Buffer, n: int):
+        """op_add_f32 / op_sub_f32 / op_mul_f32 / op_div_f32 through the vtable."""
+        self.plugin.check(self.plugin.vt_binary[op](self.handle, a.handle, b.handle, out.handle, n),
+                          f"op_{op}_f32")
+
     def matmul_f32(self, a: Buffer, b: Buffer, out: Buffer, M: int, K: int, N: int):
         self.plugin.check(self.plugin.vt_matmul(self.handle, a.handle, b.handle, out.handle, M, K, N),
                           "op_matmul_f32")
@@ -354,6 +368,14 @@ class Context:
             self.handle, byref(desc), w.handle, scales.handle if scales else None, x.handle,
             x_scales.handle if x_scales else None, epilogue, bias.handle if bias else None,
             residual.handle if residual else None, y.handle), "qmatmul_ex")
+
+    def rms_norm(self, x: Buffer, gamma: Buffer, y: Buffer, rows: int, hidden: int,
+                 eps: float = 1e-6, x_dtype: int = F32, y_dtype: int = F32,
+                 rms_out: Buffer | None = None):
+        p = RmsNormParams(rows, hidden, eps, x_dtype, y_dtype)
+        self.plugin.check(self.lib.lux_hip_rms_norm(self.handle, byref(p), x.handle, gamma.handle,
+                                                    y.handle, rms_out.handle if rms_out else None),
+                          "rms_norm")
 
     def quantize(self, desc: QuantizeDesc, x: Buffer, q: Buffer, scales: Buffer):
         self.plugin.check(self.lib.lux_hip_quantize(self.handle, byref(desc), x.handle, q.handle,

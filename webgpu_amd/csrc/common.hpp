@@ -234,6 +234,13 @@ hipError_t launch_qgemm_i4_large(const QArgs& a, void* workspace, hipStream_t s)
 bool w4a8_supported(const QArgs& a);
 hipError_t launch_w4a8(const QArgs& a, hipStream_t s);
 
+// Elementwise f32 ops of the ABI tensor slots: op 0 add, 1 sub, 2 mul, 3 div.
+hipError_t launch_binary_f32(int op, const float* a, const float* b, float* out, size_t n, hipStream_t s);
+hipError_t launch_fill_f32(float* out, size_t n, float v, hipStream_t s);
+// RMS normalisation of rows x hidden (rms_norm.wgsl); rms_out may be null.
+hipError_t launch_rms_norm(const void* x, XKind xk, const float* gamma, void* y, YKind yk, float* rms_out, int rows,
+                           int hidden, float eps, hipStream_t s);
+
 // Symmetric group quantizer (scales + packed values) over X [rows x k].
 struct QuantArgs {
     const void* x;        // [rows x k], x_kind

@@ -299,7 +299,7 @@ LuxBackendError hip_op_matmul_f32(LuxBackendContext* ctx, LuxBackendBuffer* a, L
     float* po = static_cast<float*>(O->ptr);
     hipError_t he;
     if (K == 0) {
-        he = hipMemsetAsync(po, 0, m * n * 4, c->stream);
+        he = launch_fill_f32(po, m * n, 0.0f, c->stream);
     } else if (N == 1) {
         // GEMV: C[M] = A[M x K] . B[K]  (the reference runs this through the 16x16
         // GEMM with 15/16 lanes idle, src/webgpu_plugin.cpp:1759-1763).
@@ -311,6 +311,39 @@ LuxBackendError hip_op_matmul_f32(LuxBackendContext* ctx, LuxBackendBuffer* a, L
         he = launch_gemm_f32(pa, pb, po, M, K, N, c->stream);
     }
     return end_op(c, he, "op_matmul_f32");
+}
+
+// Elementwise slots (src/webgpu_plugin.cpp:1637-1719, WGSL_BINARY_OPS :92-135): out[i] =
+// a[i] op b[i] for i < n, strides 1.  The reference leaves op_div_f32 NOT_SUPPORTED
+// (:3548); it is filled here with the same elementwise form.
+LuxBackendError hip_binary(LuxBackendContext* ctx, LuxBackendBuffer* a, LuxBackendBuffer* b, LuxBackendBuffer* out,
+                           size_t n, int op, const char* name) {
+    HipCtx* c = C(ctx);
+    HipBuf *A = B(a), *Bb = B(b), *O = B(out);
+    if (!c || !A || !Bb || !O) return fail(LUX_BACKEND_ERROR_INVALID_ARGUMENT, "%s: NULL argument", name);
+    if (!fits(A, n * 4) || !fits(Bb, n * 4) || !fits(O, n * 4))
+        return fail(LUX_BACKEND_ERROR_INVALID_ARGUMENT, "%s: buffer smaller than %zu floats", name, n);
+    if (LuxBackendError e = begin_op(c, name)) return e;
+    if (n == 0) return LUX_BACKEND_OK;
+    return end_op(c, launch_binary_f32(op, static_cast<const float*>(A->ptr), static_cast<const float*>(Bb->ptr),
+                                       static_cast<float*>(O->ptr), n, c->stream),
+                  name);
+}
+LuxBackendError hip_op_add_f32(LuxBackendContext* c, LuxBackendBuffer* a, LuxBackendBuffer* b, LuxBackendBuffer* o,
+                               size_t n) {
+    return hip_binary(c, a, b, o, n, 0, "op_add_f32");
+}
+LuxBackendError hip_op_sub_f32(LuxBackendContext* c, LuxBackendBuffer* a, LuxBackendBuffer* b, LuxBackendBuffer* o,
+                               size_t n) {
+    return hip_binary(c, a, b, o, n, 1, "op_sub_f32");
+}
+LuxBackendError hip_op_mul_f32(LuxBackendContext* c, LuxBackendBuffer* a, LuxBackendBuffer* b, LuxBackendBuffer* o,
+                               size_t n) {
+    return hip_binary(c, a, b, o, n, 2, "op_mul_f32");
+}
+LuxBackendError hip_op_div_f32(LuxBackendContext* c, LuxBackendBuffer* a, LuxBackendBuffer* b, LuxBackendBuffer* o,
+                               size_t n) {
+    return hip_binary(c, a, b, o, n, 3, "op_div_f32");
 }
 
 // ---------------------------------------------------------------- vtable
@@ -328,6 +361,10 @@ const lux_gpu_backend_vtbl g_vtbl = [] {
     v.buffer_copy_to_host = hip_buffer_copy_to_host;
     v.buffer_copy_from_host = hip_buffer_copy_from_host;
     v.buffer_get_host_ptr = hip_buffer_get_host_ptr;
+    v.op_add_f32 = hip_op_add_f32;
+    v.op_sub_f32 = hip_op_sub_f32;
+    v.op_mul_f32 = hip_op_mul_f32;
+    v.op_div_f32 = hip_op_div_f32;
     v.op_matmul_f32 = hip_op_matmul_f32;
     return v;
 }();
@@ -684,6 +721,34 @@ LUX_EXPORT LuxBackendError lux_hip_convert_scales(LuxBackendContext* ctx, LuxBac
 
 // requantize_int32_to_int8 (quantized.wgsl:560-580): RequantParams {size, input_scale,
 // output_scale, output_zero_point}; i32 in, i32 out clamped to [-128, 127].
+// rms_norm.wgsl:25-110 (RMSNormParams {batch_size, hidden_size, eps}; bindings input,
+// output, gamma, rms_out).  The ABI-v3 slot op_rms_norm_f32 exists but its signature is
+// not recoverable (the reference leaves it NULL, src/webgpu_plugin.cpp:4072), so the
+// kernel is exposed here.
+LUX_EXPORT LuxBackendError lux_hip_rms_norm(LuxBackendContext* ctx, const LuxHipRmsNormParams* p,
+                                            LuxBackendBuffer* input, LuxBackendBuffer* gamma,
+                                            LuxBackendBuffer* output, LuxBackendBuffer* rms_out) {
+    HipCtx* c = C(ctx);
+    HipBuf *X = B(input), *G = B(gamma), *Y = B(output), *R = B(rms_out);
+    if (!c || !p || !X || !G || !Y) return fail(LUX_BACKEND_ERROR_INVALID_ARGUMENT, "rms_norm: NULL argument");
+    const size_t xb = dtype_bytes(p->x_dtype), yb = dtype_bytes(p->y_dtype);
+    if (!xb || !yb || p->x_dtype == LUX_HIP_I32 || p->x_dtype == LUX_HIP_I8 || p->y_dtype == LUX_HIP_I32 ||
+        p->y_dtype == LUX_HIP_I8)
+        return fail(LUX_BACKEND_ERROR_NOT_SUPPORTED, "rms_norm: dtypes must be F32, F16 or BF16");
+    if (p->hidden_size == 0 && p->batch_size != 0)
+        return fail(LUX_BACKEND_ERROR_INVALID_ARGUMENT, "rms_norm: hidden_size 0");
+    const size_t n = (size_t)p->batch_size * p->hidden_size;
+    if (!fits(X, n * xb) || !fits(Y, n * yb) || !fits(G, (size_t)p->hidden_size * 4) ||
+        (R && !fits(R, (size_t)p->batch_size * 4)))
+        return fail(LUX_BACKEND_ERROR_INVALID_ARGUMENT, "rms_norm: buffer too small");
+    if (LuxBackendError e = begin_op(c, "rms_norm")) return e;
+    if (n == 0) return LUX_BACKEND_OK;
+    return end_op(c, launch_rms_norm(X->ptr, static_cast<XKind>(p->x_dtype), static_cast<const float*>(G->ptr), Y->ptr,
+                                     static_cast<YKind>(p->y_dtype), R ? static_cast<float*>(R->ptr) : nullptr,
+                                     (int)p->batch_size, (int)p->hidden_size, p->eps, c->stream),
+                  "rms_norm");
+}
+
 LUX_EXPORT LuxBackendError lux_hip_requantize_i32(LuxBackendContext* ctx, LuxBackendBuffer* in,
                                                   LuxBackendBuffer* out, size_t size, float input_scale,
                                                   float output_scale, int32_t output_zero_point) {

@@ -13,18 +13,21 @@
 //                              group order g = 0 .. G-1.
 //
 // Tiling (gfx950, v_mfma_i32_16x16x64_i8, A = weight rows, B = tokens, K = 64):
-//   block = 4 waves = 128 weight rows x 64 tokens; wave = 32 rows (2 row tiles) x 64
-//   tokens (4 token tiles).  Per 128-k stage a lane (row l % 16, quarter q = l / 16)
-//   loads 16 packed bytes per row tile = k 32 q .. 32 q + 31 and sign-extends the
-//   nibbles into bytes with a SWAR add/xor, in the order (k0 k2 k4 k6 | k1 k3 k5 k7)
-//   per 8 k; the two MFMA k-steps take nibbles 0-15 and 16-31.  Activations of the
-//   stage (64 tokens x 128 B) are loaded as coalesced 16-B chunks one stage ahead,
+//   block = 4 waves = 64 weight rows x 64 tokens; wave = 16 rows (one row tile) x 64
+//   tokens (4 token tiles, 4 independent MFMA chains).  Small blocks let up to three
+//   of them share a CU (config 5: 688 blocks on 256 CUs), so one block's barrier and
+//   memory waits overlap another's MFMAs.  Per 128-k stage a lane (row l % 16,
+//   quarter q = l / 16) loads 16 packed bytes per row tile = k 32 q .. 32 q + 31 and
+//   sign-extends the nibbles into bytes with a SWAR add/xor, in the order
+//   (k0 k2 k4 k6 | k1 k3 k5 k7) per 8 k; the two MFMA k-steps take nibbles 0-15 and
+//   16-31.  Activations of the stage (64 tokens x 128 B) are loaded as coalesced
+//   16-B chunks PD stages ahead,
 //   byte-permuted into the same order and written to LDS; all four waves read them.
 //   The weights are the only operand each wave owns, so nothing is decoded twice.
 //
 // Block order is XCD-aware: consecutive workgroups go to the 8 XCDs in turn, so the
 // token blocks of one row block are given block ids that land on the same XCD and
-// share its L2 copy of the 128 weight rows.
+// share its L2 copy of the block's weight rows.
 #include <algorithm>
 
 #include "common.hpp"
@@ -35,12 +38,13 @@ namespace {
 
 constexpr int GK = 128;    // k per stage (one group of 128 when gs == 128)
 constexpr int AROW = GK + 16;  // LDS bytes per staged token row (padded)
-constexpr int BR = 128;    // weight rows per block
+constexpr int RT = 1;      // 16-row MFMA tiles per wave
+constexpr int BR = 64 * RT;  // weight rows per block (4 waves)
 constexpr int BT = 64;     // tokens per block
 constexpr int NXCD = 8;
-constexpr int PD = 4;      // stages fetched ahead
+constexpr int PD = 3;      // stages fetched ahead
 constexpr int GMAX = 128;  // groups per row held in LDS (scaled output)
-constexpr int SCH = 16;    // 16-byte scale chunks per thread (block region <= 64 KB)
+constexpr int SCH = 8;     // 16-byte scale chunks per thread (block region <= 32 KB)
 
 // 8 nibbles (k0..k7) of one word -> signed bytes (k0, k2, k4, k6) and (k1, k3, k5, k7).
 // Offset-binary u = q + 8: byte = (u + 0x78) ^ 0x80.  Two's complement t: u = t ^ 8,
@@ -70,7 +74,7 @@ __device__ __forceinline__ u32x4 perm16(u32x4 v) {
 // MODE 0: full-K int32; 1: per-group int32 partials; 2: scaled fp output.
 // ONEG: group size == 128, every stage is one whole group (no carry across stages).
 template <int MODE, bool ONEG, ScaleKind SK, YKind YK>
-__global__ __launch_bounds__(256) void k_w4a8(const uint8_t* __restrict__ W,
+__global__ __launch_bounds__(256, MODE == 1 ? 2 : 3) void k_w4a8(const uint8_t* __restrict__ W,
                                               const void* __restrict__ S,
                                               const int8_t* __restrict__ A,
                                               const float* __restrict__ AS,
@@ -83,7 +87,7 @@ __global__ __launch_bounds__(256) void k_w4a8(const uint8_t* __restrict__ W,
     const int b = blockIdx.x, j = b / NXCD;
     const int rb = (j / ntb) * NXCD + b % NXCD, tbk = j % ntb;
     if (rb >= nrb) return;  // whole block: no barrier is skipped by part of it
-    const int n0 = rb * BR + wv * 32;  // first weight row of the wave
+    const int n0 = rb * BR + wv * 16 * RT;  // first weight row of the wave
     const int tb = tbk * BT;           // first token of the block
     const int r16 = lane & 15, q = lane >> 4;
     const int G = K / gs;
@@ -97,16 +101,17 @@ __global__ __launch_bounds__(256) void k_w4a8(const uint8_t* __restrict__ W,
         __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(W), (short)0, (int)((size_t)N * K / 2), 0x00020000);
     const __amdgpu_buffer_rsrc_t ra =
         __builtin_amdgcn_make_buffer_rsrc(const_cast<int8_t*>(A), (short)0, (int)((size_t)M * K), 0x00020000);
-    const int wv0 = (n0 + r16) * (K / 2) + 16 * q, wv1 = wv0 + 16 * (K / 2);
+    const int wv0 = (n0 + r16) * (K / 2) + 16 * q;
     // activation chunks of a stage: 64 tokens x 8 chunks of 16 B; thread: token tid / 8
     // and tid / 8 + 32, chunk tid % 8 (8 lanes read one token's 128 contiguous bytes)
     const int tk = tid >> 3, part = tid & 7;
     const int av0 = (tb + tk) * K + 16 * part, av1 = av0 + 32 * K;
 
-    auto ldw = [&](u32x4 (&w)[2], int st) {
+    auto ldw = [&](u32x4 (&w)[RT], int st) {
         const int so = __builtin_amdgcn_readfirstlane(st * (GK / 2));
-        w[0] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rw, wv0, so, 0));
-        w[1] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rw, wv1, so, 0));
+#pragma unroll
+        for (int f = 0; f < RT; ++f)
+            w[f] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rw, wv0 + f * 16 * (K / 2), so, 0));
     };
     auto lda = [&](u32x4 (&a)[2], int st) {
         const int so = __builtin_amdgcn_readfirstlane(st * GK);
@@ -118,10 +123,10 @@ __global__ __launch_bounds__(256) void k_w4a8(const uint8_t* __restrict__ W,
         *reinterpret_cast<u32x4*>(&as[buf][tk + 32][16 * part]) = perm16(a[1]);
     };
 
-    i32x4 iacc[2][4];
-    f32x4 facc[2][4];
+    i32x4 iacc[RT][4];
+    f32x4 facc[RT][4];
 #pragma unroll
-    for (int f = 0; f < 2; ++f)
+    for (int f = 0; f < RT; ++f)
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
             iacc[f][t] = i32x4{0, 0, 0, 0};
@@ -142,15 +147,14 @@ __global__ __launch_bounds__(256) void k_w4a8(const uint8_t* __restrict__ W,
 #pragma unroll
         for (int c = 0; c < SCH; ++c) {
             const int ch = tid + 256 * c;
-            // unconditional: chunks past the region are read but never used
-            sv[c] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, base + 16 * ch, 0, 0));
+            if (ch < nch) sv[c] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, base + 16 * ch, 0, 0));
         }
     }
     // Weights and activations of stage st + PD are fetched while stage st computes:
     // PD register sets, the loop unrolled by PD so each set is a fixed set of
     // registers.  Set i: W[i] holds the weights of the stage it serves; A[i] its
     // activations, written to LDS at the end of the previous stage.
-    u32x4 Wr[PD][2], Ar[PD][2];
+    u32x4 Wr[PD][RT], Ar[PD][2];
 #pragma unroll
     for (int i = 0; i < PD; ++i) {
         ldw(Wr[i], i);
@@ -161,12 +165,16 @@ __global__ __launch_bounds__(256) void k_w4a8(const uint8_t* __restrict__ W,
         for (int c = 0; c < SCH; ++c) {
             const int ch = tid + 256 * c;
             if (ch < nch) {
+                int row = ch * EPC / G, g = ch * EPC % G;  // walked forward: one division per chunk
 #pragma unroll
                 for (int e = 0; e < EPC; ++e) {
-                    const int idx = ch * EPC + e, row = idx / G, g = idx % G;
                     const uint32_t wd = sv[c][SK == ScaleKind::F16 ? e / 2 : e];
                     const uint32_t raw = SK == ScaleKind::F16 ? (wd >> (16 * (e & 1))) & 0xFFFFu : wd;
                     ssT[g * BR + row] = scale_from_raw<SK>(raw);
+                    if (++g == G) {
+                        g = 0;
+                        ++row;
+                    }
                 }
             }
         }
@@ -174,19 +182,17 @@ __global__ __launch_bounds__(256) void k_w4a8(const uint8_t* __restrict__ W,
     sta(0, Ar[0]);
     __syncthreads();
 
-    auto stage = [&](int st, u32x4 (&wc)[2], u32x4 (&ac)[2], const u32x4 (&an)[2]) {
+    auto stage = [&](int st, u32x4 (&wc)[RT], u32x4 (&ac)[2], const u32x4 (&an)[2]) {
         const int buf = st & 1;
         const int k0 = st * GK;
         const bool gstart = ONEG || k0 % gs == 0, gend = ONEG || (k0 + GK) % gs == 0;
         const int g = ONEG ? st : k0 / gs;
-        uint32_t b8[2][8];
-        {
-            const uint32_t ww[2][4] = {{wc[0].x, wc[0].y, wc[0].z, wc[0].w},
-                                       {wc[1].x, wc[1].y, wc[1].z, wc[1].w}};
+        uint32_t b8[RT][8];
 #pragma unroll
-            for (int f = 0; f < 2; ++f)
+        for (int f = 0; f < RT; ++f) {
+            const uint32_t ww[4] = {wc[f].x, wc[f].y, wc[f].z, wc[f].w};
 #pragma unroll
-                for (int i = 0; i < 4; ++i) unpack_i4_to_i8(ww[f][i], tc, b8[f][2 * i], b8[f][2 * i + 1]);
+            for (int i = 0; i < 4; ++i) unpack_i4_to_i8(ww[i], tc, b8[f][2 * i], b8[f][2 * i + 1]);
         }
         ldw(wc, st + PD);
         lda(ac, st + PD);
@@ -199,23 +205,23 @@ __global__ __launch_bounds__(256) void k_w4a8(const uint8_t* __restrict__ W,
             bk[t][0] = *reinterpret_cast<const i32x4*>(arow);
             bk[t][1] = *reinterpret_cast<const i32x4*>(arow + 16);
         }
-        f32x4 sc[2];
+        f32x4 sc[RT];
         if constexpr (MODE == 2) {
             // scales of this lane's D rows 16 f + 4 q + r for the group
 #pragma unroll
-            for (int f = 0; f < 2; ++f) sc[f] = *reinterpret_cast<const f32x4*>(&ssT[g * BR + wv * 32 + 16 * f + 4 * q]);
+            for (int f = 0; f < RT; ++f) sc[f] = *reinterpret_cast<const f32x4*>(&ssT[g * BR + wv * 16 * RT + 16 * f + 4 * q]);
         }
-        i32x4 p[2][4];
+        i32x4 p[RT][4];
 #pragma unroll
         for (int t = 0; t < 4; ++t)
 #pragma unroll
-            for (int f = 0; f < 2; ++f) p[f][t] = (MODE == 0 || !gstart) ? iacc[f][t] : i32x4{0, 0, 0, 0};
+            for (int f = 0; f < RT; ++f) p[f][t] = (MODE == 0 || !gstart) ? iacc[f][t] : i32x4{0, 0, 0, 0};
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
             for (int t = 0; t < 4; ++t)
 #pragma unroll
-                for (int f = 0; f < 2; ++f) {
+                for (int f = 0; f < RT; ++f) {
                     const i32x4 a = i32x4{(int)b8[f][4 * ks], (int)b8[f][4 * ks + 1], (int)b8[f][4 * ks + 2],
                                           (int)b8[f][4 * ks + 3]};
                     p[f][t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, bk[t][ks], p[f][t], 0, 0, 0);
@@ -223,7 +229,7 @@ __global__ __launch_bounds__(256) void k_w4a8(const uint8_t* __restrict__ W,
 #pragma unroll
         for (int t = 0; t < 4; ++t)
 #pragma unroll
-            for (int f = 0; f < 2; ++f) {
+            for (int f = 0; f < RT; ++f) {
                 if (MODE == 0 || !ONEG) iacc[f][t] = p[f][t];
                 if constexpr (MODE == 1) {
                     // P[m][n][g]: D row (weight) 16 f + 4 q + r, column (token) r16
@@ -263,7 +269,7 @@ __global__ __launch_bounds__(256) void k_w4a8(const uint8_t* __restrict__ W,
             if (m >= M) continue;
             const float asc = MODE == 2 ? AS[m] : 1.0f;
 #pragma unroll
-            for (int f = 0; f < 2; ++f) {
+            for (int f = 0; f < RT; ++f) {
                 const int n = n0 + 16 * f + 4 * q;
                 if (n >= N) continue;
                 const bool full = vec_n && n + 3 < N;

@@ -10,7 +10,7 @@ import pytest
 
 import oracle
 import webgpu_amd as W
-from util import compare, int4_weights, quantize_rows_int8, rng, round_to
+from util import bf16_to_f32, compare, int4_weights, quantize_rows_int8, rng, round_to
 
 pytestmark = pytest.mark.gpu
 
@@ -67,6 +67,38 @@ def test_config5_scaled(ctx, y):
     ref = (P * s.astype(np.float64)[None, :, :]).sum(axis=2) * ascale.astype(np.float64)[:, None]
     st = compare(got, round_to(ref.astype(np.float32), y), f"C5 scaled {y}")
     print(f"C5 {y} rel-L2 {st['rel_l2']:.3e}")
+
+
+@pytest.mark.parametrize("n_out,K,m,gs,sfmt,y", [
+    (70, 512, 20, 256, W.SCALE_F32, "bf16"),       # groups of two stages, ragged rows
+    (200, 1024, 65, 128, W.SCALE_GROUPSCALE, "f32"),  # a second 64-token block of one token
+    (64, 256, 9, 128, W.SCALE_F16, "f16"),         # two stages: fewer than the prefetch depth
+    (130, 384, 3, 128, W.SCALE_F16, "f32")])       # three stages, rows past the last block
+def test_w4a8_scaled_shapes(ctx, n_out, K, m, gs, sfmt, y):
+    """Scaled output on ragged shapes and every scale format: y = a_s[m] * sum_g s[n,g] P_g,
+    P_g from the brute-force int64 group sums."""
+    r = rng(n_out * 3 + K + m)
+    q, Wp, s16, a8, ascale = _inputs(r, n_out, K, m, gs, 1)
+    s32 = r.uniform(0.005, 0.02, size=s16.shape).astype(np.float32)
+    if sfmt == W.SCALE_F16:
+        sbuf, sref = s16, s16.astype(np.float64)
+    elif sfmt == W.SCALE_F32:
+        sbuf, sref = s32, s32.astype(np.float64)
+    else:  # GroupScale {scale, zero_point, min, max}
+        sbuf = np.zeros(s32.shape + (4,), np.float32)
+        sbuf[..., 0], sbuf[..., 2], sbuf[..., 3] = s32, -1.0, 1.0
+        sref = s32.astype(np.float64)
+    ycode, ynp = {"f16": (W.F16, np.float16), "f32": (W.F32, np.float32), "bf16": (W.BF16, np.uint16)}[y]
+    d = W.qdesc(n_out, K, m, 4, gs, 1, sfmt, W.I8, ycode)
+    yb = ctx.alloc(m * n_out * np.dtype(ynp).itemsize)
+    ctx.qmatmul(d, ctx.upload(Wp), ctx.upload(sbuf), ctx.upload(a8), ctx.upload(ascale), yb)
+    got = ctx.download(yb, ynp, (m, n_out))
+    got = (bf16_to_f32(got) if y == "bf16" else got.astype(np.float32)).astype(np.float64)
+    qg = q.reshape(n_out, K // gs, gs).astype(np.int64)
+    ag = a8.reshape(m, K // gs, gs).astype(np.int64)
+    P = np.einsum("ngk,mgk->mng", qg, ag).astype(np.float64)              # exact group sums
+    ref = (P * sref[None, :, :]).sum(axis=2) * ascale.astype(np.float64)[:, None]
+    compare(got, round_to(ref.astype(np.float32), y), f"W4A8 scaled {n_out}x{K} m{m} g{gs} {y}")
 
 
 def test_w4a8_rejects(ctx):

@@ -719,8 +719,6 @@ LUX_EXPORT LuxBackendError lux_hip_convert_scales(LuxBackendContext* ctx, LuxBac
                   "convert_scales");
 }
 
-// requantize_int32_to_int8 (quantized.wgsl:560-580): RequantParams {size, input_scale,
-// output_scale, output_zero_point}; i32 in, i32 out clamped to [-128, 127].
 // rms_norm.wgsl:25-110 (RMSNormParams {batch_size, hidden_size, eps}; bindings input,
 // output, gamma, rms_out).  The ABI-v3 slot op_rms_norm_f32 exists but its signature is
 // not recoverable (the reference leaves it NULL, src/webgpu_plugin.cpp:4072), so the
@@ -737,6 +735,8 @@ LUX_EXPORT LuxBackendError lux_hip_rms_norm(LuxBackendContext* ctx, const LuxHip
         return fail(LUX_BACKEND_ERROR_NOT_SUPPORTED, "rms_norm: dtypes must be F32, F16 or BF16");
     if (p->hidden_size == 0 && p->batch_size != 0)
         return fail(LUX_BACKEND_ERROR_INVALID_ARGUMENT, "rms_norm: hidden_size 0");
+    if (p->batch_size > INT32_MAX || p->hidden_size > INT32_MAX)
+        return fail(LUX_BACKEND_ERROR_INVALID_ARGUMENT, "rms_norm: size too large");
     const size_t n = (size_t)p->batch_size * p->hidden_size;
     if (!fits(X, n * xb) || !fits(Y, n * yb) || !fits(G, (size_t)p->hidden_size * 4) ||
         (R && !fits(R, (size_t)p->batch_size * 4)))
@@ -749,6 +749,8 @@ LUX_EXPORT LuxBackendError lux_hip_rms_norm(LuxBackendContext* ctx, const LuxHip
                   "rms_norm");
 }
 
+// requantize_int32_to_int8 (quantized.wgsl:560-580): RequantParams {size, input_scale,
+// output_scale, output_zero_point}; i32 in, i32 out clamped to [-128, 127].
 LUX_EXPORT LuxBackendError lux_hip_requantize_i32(LuxBackendContext* ctx, LuxBackendBuffer* in,
                                                   LuxBackendBuffer* out, size_t size, float input_scale,
                                                   float output_scale, int32_t output_zero_point) {

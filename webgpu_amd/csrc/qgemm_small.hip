@@ -198,8 +198,14 @@ __global__ __launch_bounds__(64 * MAXW) void k_qgemm_small(
         }
     };
 
-    // One chunk: KC k from X buffer `buf` and weight registers `slot` (static).
-    auto chunk = [&](int buf, int slot) {
+    // One chunk: KC k from X buffer `buf` and weight registers `slot` (static).  The
+    // slot's weights are decoded first, so its registers take the loads of chunk `next`
+    // before this chunk's MFMAs run: the prefetch distance is two chunks plus the MFMA
+    // and X-read time of one.
+    constexpr int SPL = WB == 8 ? 2 : 4;       // 32-k steps per load
+    auto chunk = [&](int buf, int slot, int next) {
+        f16x8 av[LPC][SPL];
+        uint32_t sc[LPC][SPLD > 0 ? SPLD : 1];
 #pragma unroll
         for (int l = 0; l < LPC; ++l) {
             const u32x4 q = wq[slot][l];
@@ -209,39 +215,37 @@ __global__ __launch_bounds__(64 * MAXW) void k_qgemm_small(
                 for (int st = 0; st < 2; ++st) {
                     const uint2 p0 = i8x4_to_f16(st ? q.z : q.x, magic);
                     const uint2 p1 = i8x4_to_f16(st ? q.w : q.y, magic);
-                    const f16x8 a = __builtin_bit_cast(f16x8, u32x4{p0.x, p0.y, p1.x, p1.y});
-#pragma unroll
-                    for (int t = 0; t < MT; ++t) {
-                        const f16x8 b = *reinterpret_cast<const f16x8*>(
-                            &xs[buf][16 * t + r16][l * KPL + 16 * kq + 8 * st]);
-                        if constexpr (PERROW) {
-                            acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, acc[t], 0, 0, 0);
-                        } else {
-                            const f32x4 p = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, f32x4{}, 0, 0, 0);
-                            // D rows 4*(lane/16) + r: scales of those rows for this group
-#pragma unroll
-                            for (int r = 0; r < 4; ++r)
-                                acc[t][r] = fmaf(p[r], scale_from_raw<SK>(sq[slot][l][r]), acc[t][r]);
-                        }
-                    }
+                    av[l][st] = __builtin_bit_cast(f16x8, u32x4{p0.x, p0.y, p1.x, p1.y});
                 }
+#pragma unroll
+                for (int r = 0; r < (SPLD > 0 ? SPLD : 1); ++r) sc[l][r] = sq[slot][l][r];
             } else {
                 // four k-steps of 32: word w covers k 32 kq + 8 w .. + 7 of this load
-                const f16 sc = (f16)scale_from_raw<SK>(sq[slot][l][0]);
-                const f16x2 s2 = {sc, sc};
+                const f16 s16 = (f16)scale_from_raw<SK>(sq[slot][l][0]);
+                const f16x2 s2 = {s16, s16};
                 const uint32_t words[4] = {q.x, q.y, q.z, q.w};
 #pragma unroll
-                for (int st = 0; st < 4; ++st) {
-                    const f16x8 a = i4x8_to_f16(words[st] ^ xor_mask, s2, magic);
-#pragma unroll
-                    for (int t = 0; t < MT; ++t) {
-                        const f16x8 b = *reinterpret_cast<const f16x8*>(
-                            &xs[buf][16 * t + r16][l * KPL + 32 * kq + 8 * st]);
-                        acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, acc[t], 0, 0, 0);
-                    }
-                }
+                for (int st = 0; st < 4; ++st) av[l][st] = i4x8_to_f16(words[st] ^ xor_mask, s2, magic);
             }
         }
+        load_w(slot, next);
+#pragma unroll
+        for (int l = 0; l < LPC; ++l)
+#pragma unroll
+            for (int st = 0; st < SPL; ++st)
+#pragma unroll
+                for (int t = 0; t < MT; ++t) {
+                    const int kx = WB == 8 ? l * KPL + 16 * kq + 8 * st : l * KPL + 32 * kq + 8 * st;
+                    const f16x8 bx = *reinterpret_cast<const f16x8*>(&xs[buf][16 * t + r16][kx]);
+                    if constexpr (WB == 4 || PERROW) {
+                        acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[l][st], bx, acc[t], 0, 0, 0);
+                    } else {
+                        const f32x4 pr = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[l][st], bx, f32x4{}, 0, 0, 0);
+                        // D rows 4*(lane/16) + r: scales of those rows for this group
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) acc[t][r] = fmaf(pr[r], scale_from_raw<SK>(sc[l][r]), acc[t][r]);
+                    }
+                }
     };
 
     // Chunks in pairs so the weight-register slots are static; weights run two chunks
@@ -253,14 +257,12 @@ __global__ __launch_bounds__(64 * MAXW) void k_qgemm_small(
     __syncthreads();
     for (int c = 0; c < nchunks; c += 2) {
         if (c + 1 < nchunks) load_xc((c + 1) * KC);
-        chunk(0, 0);
-        load_w(0, c + 2);
+        chunk(0, 0, c + 2);
         if (c + 1 < nchunks) store_xc(1);
         __syncthreads();
         if (c + 1 < nchunks) {
             if (c + 2 < nchunks) load_xc((c + 2) * KC);
-            chunk(1, 1);
-            load_w(1, c + 3);
+            chunk(1, 1, c + 3);
             if (c + 2 < nchunks) store_xc(0);
             __syncthreads();
         }

@@ -127,6 +127,7 @@ def test_config3_int8_per_row(ctx, m):
     (100, 256, 1, 256, "f16", "f32"),
     (1000, 512, 5, 512, "bf16", "bf16"),
     (513, 1024, 64, 128, "f16", "f32"),
+    (300, 512, 45, 64, "bf16", "f16"),   # group scales: a 32-token pass, then 13 tokens
     (256, 768, 70, 768, "f32", "f16"),
 ])
 def test_int8_small_shapes(ctx, n_out, K, m, gs, xd, y):

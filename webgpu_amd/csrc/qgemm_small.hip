@@ -326,21 +326,27 @@ static void launch_one(const QArgs& a, const void* x, void* y, const float* xfac
 
 template <int WB, bool PERROW, ScaleKind SK, XKind XK, YKind YK>
 static void launch_m(const QArgs& a, hipStream_t s) {
-    // m > 64: passes of 64 tokens (each re-reads the weights).
+    // m > 64: passes of 64 tokens (each re-reads the weights).  int8 with group scales
+    // takes 32 per pass: its per-step scale registers do not fit beside four m-tiles.
+    constexpr int PASS = (WB == 8 && !PERROW) ? 32 : 64;
     const size_t xel = a.x_kind == XKind::F32 ? 4 : 2;
     const size_t yel = a.y_kind == YKind::F32 ? 4 : 2;
     const int ny = a.epi.kind == (int)Epi::SiluMul ? a.n_out / 2 : a.n_out;  // output columns
-    for (int m0 = 0; m0 < a.m; m0 += 64) {
-        const int m = std::min(64, a.m - m0);
+    for (int m0 = 0; m0 < a.m; m0 += PASS) {
+        const int m = std::min(PASS, a.m - m0);
         const void* x = reinterpret_cast<const uint8_t*>(a.x) + (size_t)m0 * a.k * xel;
         void* y = reinterpret_cast<uint8_t*>(a.y) + (size_t)m0 * ny * yel;
         const float* xf = a.xfac ? a.xfac + m0 : nullptr;
         EpiArgs e = a.epi;
         if (e.residual) e.residual += (size_t)m0 * ny;
-        if (m <= 16) launch_one<WB, 1, PERROW, SK, XK, YK>(a, x, y, xf, m, e, s);
-        else if (m <= 32) launch_one<WB, 2, PERROW, SK, XK, YK>(a, x, y, xf, m, e, s);
-        else if (m <= 48) launch_one<WB, 3, PERROW, SK, XK, YK>(a, x, y, xf, m, e, s);
-        else launch_one<WB, 4, PERROW, SK, XK, YK>(a, x, y, xf, m, e, s);
+        if (m <= 16) {
+            launch_one<WB, 1, PERROW, SK, XK, YK>(a, x, y, xf, m, e, s);
+        } else if (m <= 32) {
+            launch_one<WB, 2, PERROW, SK, XK, YK>(a, x, y, xf, m, e, s);
+        } else if constexpr (PASS == 64) {
+            if (m <= 48) launch_one<WB, 3, PERROW, SK, XK, YK>(a, x, y, xf, m, e, s);
+            else launch_one<WB, 4, PERROW, SK, XK, YK>(a, x, y, xf, m, e, s);
+        }
     }
 }
 

@@ -78,13 +78,9 @@ __device__ __forceinline__ float bf16_bits_to_f32(uint32_t b) {
     return __builtin_bit_cast(float, b << 16);
 }
 
-// bfloat16 round-to-nearest-even (NaN kept quiet).
-__device__ __forceinline__ uint16_t f32_to_bf16_bits(float v) {
-    uint32_t x = __builtin_bit_cast(uint32_t, v);
-    if ((x & 0x7FFFFFFFu) > 0x7F800000u) return (uint16_t)((x >> 16) | 0x40u);
-    x += 0x7FFFu + ((x >> 16) & 1u);
-    return (uint16_t)(x >> 16);
-}
+// bfloat16 round-to-nearest-even (NaN kept quiet): the hardware conversion
+// (v_cvt_pk_bf16_f32 on gfx950), the same one store_y4 uses.
+__device__ __forceinline__ uint16_t f32_to_bf16_bits(float v) { return __builtin_bit_cast(uint16_t, (__bf16)v); }
 
 template <YKind Y>
 __device__ __forceinline__ void store_y(void* y, size_t idx, float v) {

@@ -17,6 +17,13 @@ def pytest_configure(config):
 
 @pytest.fixture(scope="session")
 def plugin():
+    # PyTorch-ROCm ships its own HIP runtime.  Loading it before the plugin makes the
+    # plugin bind to that runtime, so tests that mix torch tensors and plugin calls in
+    # one process see one HIP runtime (bench.py imports torch first for the same reason).
+    try:
+        import torch  # noqa: F401
+    except ImportError:
+        pass
     import webgpu_amd
     return webgpu_amd.Plugin()
 

@@ -1,0 +1,95 @@
+"""GPU: the asynchronous stream mode of the plugin under HIP graph capture.
+
+A caller that sets lux_hip_context_set_synchronous(ctx, 0) and its own stream may capture
+the plugin's launches in a graph (bench.py times every config that way).  One graph holds
+a decode step (rms_norm -> int4 gate/up GEMM with SILU_MUL -> int4 down GEMV -> residual
+op_add_f32), a large-m int4 GEMM with bf16 activations (pre-pass + MFMA GEMM, workspace)
+and a W4A8 GEMM with QUANTIZE_X (per-token quantizer + int8 MFMA, workspace).  It is
+replayed three times with new inputs written by eager torch work between the replays;
+every replay must equal, bit for bit, the same ops run eagerly in synchronous mode (the
+kernels are deterministic, so graph and eager results are identical).
+"""
+import numpy as np
+import pytest
+
+import webgpu_amd as W
+from util import int4_weights, rng
+
+pytestmark = pytest.mark.gpu
+
+
+def test_graph_replays_match_eager(plugin):
+    import torch
+    c = plugin.create_context(0)
+    try:
+        r = rng(4242)
+        hidden, inter, gs = 1024, 512, 32
+        x = torch.tensor(r.standard_normal(hidden), dtype=torch.float32, device="cuda")
+        gamma = torch.tensor(r.uniform(0.8, 1.2, hidden), dtype=torch.float32, device="cuda")
+        _, Wgu, sgu = int4_weights(r, 2 * inter, hidden, gs)
+        _, Wd, sd = int4_weights(r, hidden, inter, gs)
+        ml, nl, kl = 100, 256, 512                      # large-m int4 GEMM, bf16 activations
+        _, Wl, sl = int4_weights(r, nl, kl, 32)
+        xl = torch.tensor(r.standard_normal((ml, kl)), dtype=torch.bfloat16, device="cuda")
+        mq, nq, kq = 64, 256, 512                       # W4A8 with per-token quantization
+        _, Wq, sq = int4_weights(r, nq, kq, 128, 1)
+        xq = torch.tensor(r.standard_normal((mq, kq)), dtype=torch.float32, device="cuda")
+
+        xb, gb, xlb, xqb = c.wrap(x), c.wrap(gamma), c.wrap(xl), c.wrap(xq)
+        wgu, s_gu, wd, s_d = c.upload(Wgu), c.upload(sgu), c.upload(Wd), c.upload(sd)
+        wl, s_l, wq, s_q = c.upload(Wl), c.upload(sl), c.upload(Wq), c.upload(sq)
+        nb, hb = c.alloc(hidden * 2), c.alloc(inter * 2)
+        d_gu = W.qdesc(2 * inter, hidden, 1, 4, gs, 0, W.SCALE_F16, W.F16, W.F16)
+        d_d = W.qdesc(hidden, inter, 1, 4, gs, 0, W.SCALE_F16, W.F16, W.F32)
+        d_l = W.qdesc(nl, kl, ml, 4, 32, 0, W.SCALE_F16, W.BF16, W.BF16)
+        d_q = W.qdesc(nq, kq, mq, 4, 128, 1, W.SCALE_F16, W.F32, W.F16, W.QFLAG_QUANTIZE_X)
+        shapes = {"d": (hidden * 4, np.float32, (hidden,)), "res": (hidden * 4, np.float32, (hidden,)),
+                  "large": (ml * nl * 2, np.uint16, (ml, nl)), "w4a8": (mq * nq * 2, np.uint16, (mq, nq))}
+
+        def outputs():
+            return {k: c.alloc(v[0]) for k, v in shapes.items()}
+
+        def run(o):
+            c.rms_norm(xb, gb, nb, 1, hidden, 1e-6, W.F32, W.F16)
+            c.qmatmul_ex(d_gu, wgu, s_gu, nb, None, W.EPI_SILU_MUL, None, None, hb)
+            c.qmatmul(d_d, wd, s_d, hb, None, o["d"])
+            c.binary_f32("add", xb, o["d"], o["res"], hidden)
+            c.qmatmul(d_l, wl, s_l, xlb, None, o["large"])
+            c.qmatmul(d_q, wq, s_q, xqb, None, o["w4a8"])
+
+        def fetch(o):
+            return {k: c.download(o[k], v[1], v[2]) for k, v in shapes.items()}
+
+        og, oe = outputs(), outputs()
+        run(og)  # eager first: workspaces are sized outside the capture
+        s = torch.cuda.Stream()
+        c.set_stream(s.cuda_stream)
+        c.set_synchronous(False)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            run(og)
+        c.set_stream(None)
+        c.set_synchronous(True)
+
+        prev = None
+        for i in range(3):
+            # new inputs from eager torch work on the default stream
+            x.mul_(1.25).add_(0.5 * (i + 1))
+            xl.copy_(torch.tensor(r.standard_normal((ml, kl)), dtype=torch.bfloat16))
+            xq.mul_(-0.75).add_(0.25)
+            torch.cuda.synchronize()
+            with torch.cuda.stream(s):
+                g.replay()
+            torch.cuda.synchronize()
+            got = fetch(og)
+            run(oe)  # the same ops, synchronous, on the context's own stream
+            ref = fetch(oe)
+            for k in shapes:
+                assert np.array_equal(got[k].view(np.uint8), ref[k].view(np.uint8)), f"replay {i}: {k}"
+            if prev is not None:  # the replay saw the new inputs
+                assert not np.array_equal(got["res"], prev["res"])
+                assert not np.array_equal(got["large"], prev["large"])
+                assert not np.array_equal(got["w4a8"], prev["w4a8"])
+            prev = got
+    finally:
+        c.close()

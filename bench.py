@@ -38,20 +38,33 @@ C5 = dict(n_out=11008, k=4096, m=256, gs=128)
 INT8_MFMA_PEAK_TOPS = 5000.0
 COPY_BYTES = 512 * 2**20
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "hbm_traffic.md")
+MFMA_FILE = os.path.join(ROOT, "profiles", "mfma_utilization.md")
+
+
+def _profile_value(path: str, tag: str, key: str, cast):
+    """A `<tag> <key>: <value>` line of a committed rocprofv3 summary; None when absent."""
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.startswith(f"{tag} {key}:"):
+                    return cast(line.split(":", 1)[1].strip().split()[0])
+    except OSError:
+        pass
+    return None
 
 
 def measured_traffic(key: str):
     """HBM bytes per launch measured with rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE
     (scaled by the copy-kernel calibration), recorded in profiles/hbm_traffic.md as
     a line `traffic <key>: <bytes>`; None when not recorded."""
-    try:
-        with open(TRAFFIC_FILE) as f:
-            for line in f:
-                if line.startswith(f"traffic {key}:"):
-                    return int(line.split(":", 1)[1].strip().split()[0])
-    except OSError:
-        pass
-    return None
+    return _profile_value(TRAFFIC_FILE, "traffic", key, int)
+
+
+def measured_mfma_busy(key: str):
+    """Fraction of the kernel's cycles with the matrix pipes busy, from rocprofv3 --pmc
+    SQ_VALU_MFMA_BUSY_CYCLES / (1024 SIMDs x GRBM_GUI_ACTIVE / 8), recorded in
+    profiles/mfma_utilization.md as `mfma_busy <key>: <fraction>`; None when absent."""
+    return _profile_value(MFMA_FILE, "mfma_busy", key, float)
 
 
 def log(msg):
@@ -217,7 +230,7 @@ def bench_c5(torch, W, ctx, steps, warmup):
             "hbm_gbs": round(nbytes / per / 1e9, 2),
             "roofline": {"bound": "mfma", "achieved": round(tops, 2), "peak": INT8_MFMA_PEAK_TOPS,
                          "unit": "TOP/s", "frac": round(tops / INT8_MFMA_PEAK_TOPS, 4),
-                         "traffic": measured_traffic("c5")}}
+                         "traffic": measured_traffic("c5"), "mfma_busy": measured_mfma_busy("c5")}}
 
 
 QW_BYTES = 14336 * 4096 * 4 + 14336 * 4096 // 2 + 14336 * (4096 // 32) * 2  # read f32, write int4 + f16 scales
@@ -407,7 +420,8 @@ def main():
             "us_per_launch": round(c4["per_launch_s"] * 1e6, 2),
             "roofline": {"bound": "mfma", "achieved": round(c4["tflops"], 2),
                          "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s",
-                         "frac": round(c4["frac"], 4), "traffic": measured_traffic("c4")}},
+                         "frac": round(c4["frac"], 4), "traffic": measured_traffic("c4"),
+                         "mfma_busy": measured_mfma_busy("c4")}},
         "fp32_gemv_c1": c1,
         "int8_gemm_c3": c3s or None,
         "w4a8_gemm_c5": c5,

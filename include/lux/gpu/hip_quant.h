@@ -59,7 +59,7 @@ typedef enum LuxHipScaleFormat {
                                      (quantized_nax.wgsl:49-54); only .scale used */
 } LuxHipScaleFormat;
 
-/* Descriptor of one weight-only (or W4A8) quantized matmul
+/* Descriptor of one weight-only (or W4A8 / W8A8) quantized matmul
  *   Y[m, n] = sx[m] * sum_k (q(n, k) * s(n, k / group_size)) * X[m, k]
  * sx is 1 unless X is int8 with per-token scales. */
 typedef struct LuxHipQMatmulDesc {
@@ -71,19 +71,19 @@ typedef struct LuxHipQMatmulDesc {
     int32_t group_size;     /* k elements per scale along k; k for per-row scales */
     int32_t nibble_coding;  /* LuxHipNibbleCoding (4-bit weights only)            */
     int32_t scale_format;   /* LuxHipScaleFormat                                   */
-    int32_t x_dtype;        /* F16, BF16, F32, or I8 (W4A8)                        */
-    int32_t y_dtype;        /* F16, BF16, F32, or I32 (W4A8 integer sums)          */
+    int32_t x_dtype;        /* F16, BF16, F32, or I8 (W4A8 / W8A8)                 */
+    int32_t y_dtype;        /* F16, BF16, F32, or I32 (W4A8 / W8A8 integer sums)   */
     int32_t flags;          /* LUX_HIP_QFLAG_*                                     */
 } LuxHipQMatmulDesc;
 
-/* W4A8 with y_dtype I32 and group_size < k: write the per-group int32 partial
+/* W4A8 / W8A8 with y_dtype I32 and group_size < k: write the per-group int32 partial
  * sums P[m][n][g] instead of the full-k sum (checking aid, bit-exact). */
 #define LUX_HIP_QFLAG_GROUP_PARTIALS (1 << 0)
-/* W4A8 from fp activations: x_dtype F32/F16/BF16 is quantized per token to int8 first
+/* W4A8 / W8A8 from fp activations: x_dtype F32/F16/BF16 is quantized per token to int8 first
  * (compute_group_scales NAX_INT8_SYM + quantize_nax_int8_group with group_size = k,
  * quantized_nax.wgsl:157-232,336-362; s = max|row| / 127, q = clamp(round(x / s)))
  * into the context workspace, then multiplied on the int8 MFMA as with x_dtype I8 and
- * x_scales = s.  Needs weight_bits 4, group scales, an fp y_dtype and x_scales NULL. */
+ * x_scales = s.  Needs weight scales, an fp y_dtype and x_scales NULL. */
 #define LUX_HIP_QFLAG_QUANTIZE_X (1 << 1)
 
 /* Quantized matmul / GEMV.  Replaces, by descriptor:
@@ -93,6 +93,8 @@ typedef struct LuxHipQMatmulDesc {
  *                       src/webgpu_plugin.cpp:138-205  (weight_bits 8)
  *   matmul_int4_int8    quantized.wgsl:590-647  (weight_bits 4, two's complement,
  *                       x_dtype I8, y_dtype I32, SCALE_NONE)
+ *   matmul_int8         quantized.wgsl:497-555  (weight_bits 8, x_dtype I8,
+ *                       y_dtype I32, SCALE_NONE; k % 128 == 0)
  * x_scales is read only for x_dtype I8 with y_dtype != I32 (f32 [m]); pass NULL
  * otherwise.  Returns INVALID_ARGUMENT for NULL handles, buffers smaller than the
  * descriptor implies or inconsistent sizes, NOT_SUPPORTED for combinations without

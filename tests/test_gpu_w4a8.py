@@ -10,7 +10,7 @@ import pytest
 
 import oracle
 import webgpu_amd as W
-from util import bf16_to_f32, compare, int4_weights, quantize_rows_int8, rng, round_to
+from util import bf16_to_f32, compare, int4_weights, int8_weights, quantize_rows_int8, rng, round_to
 
 pytestmark = pytest.mark.gpu
 
@@ -147,3 +147,65 @@ def test_w4a8_quantize_x(ctx, xdt):
     with pytest.raises(W.LuxError):  # x_scales must not be passed with QUANTIZE_X
         ctx.qmatmul(W.qdesc(n_out, K, m, 4, gs, 1, W.SCALE_F16, code, W.F16, W.QFLAG_QUANTIZE_X),
                     wb, sb, ctx.upload(xin), ctx.upload(ascale), y1)
+
+
+# --------------------------------------------------------------------------- W8A8
+@pytest.mark.parametrize("n_out,K,m", [(512, 4096, 256), (97, 512, 300), (40, 256, 3)])
+def test_w8a8_full_k_int32_exact(ctx, n_out, K, m):
+    """int8 weights x int8 activations, full-K int32 sums: matmul_int8
+    (quantized.wgsl:497-555) restated in oracle/lux_oracle.c, bit-exact; an independent
+    int64 numpy product on top."""
+    r = rng(3 * n_out + K + m)
+    q, _ = int8_weights(r, n_out, K)
+    a8, _ = quantize_rows_int8(r.standard_normal((m, K)).astype(np.float32))
+    d = W.qdesc(n_out, K, m, 8, K, 0, W.SCALE_NONE, W.I8, W.I32)
+    yb = ctx.alloc(m * n_out * 4)
+    ctx.qmatmul(d, ctx.upload(q), None, ctx.upload(a8), None, yb)
+    got = ctx.download(yb, np.int32, (m, n_out))
+    ref = oracle.matmul_int8(q, np.ascontiguousarray(a8.T)).T  # [m, n]
+    assert np.array_equal(got, ref)
+    assert np.array_equal(got, (a8.astype(np.int64) @ q.astype(np.int64).T).astype(np.int32))
+
+
+@pytest.mark.parametrize("n_out,K,m,gs,sfmt,y", [
+    (1024, 4096, 256, 4096, W.SCALE_F16, "f16"),  # per-output-channel scales
+    (300, 1024, 70, 128, W.SCALE_F32, "bf16"),    # group scales, ragged rows and tokens
+])
+def test_w8a8_scaled(ctx, n_out, K, m, gs, sfmt, y):
+    """Scaled output y = a_s[m] * sum_g s[n,g] P_g[m,n] with int8 weights, P_g exact."""
+    r = rng(n_out + 5 * m)
+    q, _ = int8_weights(r, n_out, K)
+    s = r.uniform(0.001, 0.01, size=(n_out, K // gs)).astype(np.float32)
+    sbuf = s.astype(np.float16) if sfmt == W.SCALE_F16 else s
+    sref = sbuf.astype(np.float64)
+    a8, ascale = quantize_rows_int8(r.standard_normal((m, K)).astype(np.float32))
+    ycode, ynp = {"f16": (W.F16, np.float16), "bf16": (W.BF16, np.uint16)}[y]
+    d = W.qdesc(n_out, K, m, 8, gs, 0, sfmt, W.I8, ycode)
+    yb = ctx.alloc(m * n_out * 2)
+    ctx.qmatmul(d, ctx.upload(q), ctx.upload(sbuf), ctx.upload(a8), ctx.upload(ascale), yb)
+    got = ctx.download(yb, ynp, (m, n_out))
+    got = (bf16_to_f32(got) if y == "bf16" else got.astype(np.float32)).astype(np.float64)
+    qg = q.reshape(n_out, K // gs, gs).astype(np.int64)
+    ag = a8.reshape(m, K // gs, gs).astype(np.int64)
+    P = np.einsum("ngk,mgk->mng", qg, ag).astype(np.float64)
+    ref = (P * sref[None, :, :]).sum(axis=2) * ascale.astype(np.float64)[:, None]
+    compare(got, round_to(ref.astype(np.float32), y), f"W8A8 scaled {n_out}x{K} m{m} g{gs}")
+
+
+def test_w8a8_quantize_x(ctx):
+    """QUANTIZE_X with int8 weights: bit-identical to the host-quantized int8 path."""
+    r = rng(88)
+    n_out, K, m = 512, 2048, 64
+    q, s = int8_weights(r, n_out, K)
+    x = r.standard_normal((m, K)).astype(np.float32)
+    a8, ascale = quantize_rows_int8(x)
+    wb, sb = ctx.upload(q), ctx.upload(s)
+    y1, y2 = ctx.alloc(m * n_out * 4), ctx.alloc(m * n_out * 4)
+    ctx.qmatmul(W.qdesc(n_out, K, m, 8, K, 0, W.SCALE_F16, W.F32, W.F32, W.QFLAG_QUANTIZE_X),
+                wb, sb, ctx.upload(x), None, y1)
+    ctx.qmatmul(W.qdesc(n_out, K, m, 8, K, 0, W.SCALE_F16, W.I8, W.F32), wb, sb, ctx.upload(a8),
+                ctx.upload(ascale), y2)
+    got = ctx.download(y1, np.float32, (m, n_out))
+    assert np.array_equal(got.view(np.uint32), ctx.download(y2, np.float32, (m, n_out)).view(np.uint32))
+    ref = (a8.astype(np.float64) @ q.astype(np.float64).T) * s.astype(np.float64).T * ascale.astype(np.float64)[:, None]
+    compare(got.astype(np.float64), ref, "W8A8 QUANTIZE_X")

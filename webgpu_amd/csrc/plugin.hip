@@ -504,11 +504,10 @@ LuxBackendError qmatmul_impl(LuxBackendContext* ctx, const LuxHipQMatmulDesc* d,
     if (K % 32 != 0) return fail(LUX_BACKEND_ERROR_NOT_SUPPORTED, "qmatmul: k %% 32 != 0");
     // QUANTIZE_X: fp activations are quantized per token to int8 first (W4A8 prologue)
     const bool qx = (d->flags & LUX_HIP_QFLAG_QUANTIZE_X) != 0;
-    if (qx && !(d->weight_bits == 4 && (d->x_dtype == LUX_HIP_F32 || d->x_dtype == LUX_HIP_F16 ||
-                                         d->x_dtype == LUX_HIP_BF16) &&
+    if (qx && !((d->x_dtype == LUX_HIP_F32 || d->x_dtype == LUX_HIP_F16 || d->x_dtype == LUX_HIP_BF16) &&
                 d->y_dtype != LUX_HIP_I32 && d->scale_format != LUX_HIP_SCALE_NONE && !x_scales))
         return fail(LUX_BACKEND_ERROR_INVALID_ARGUMENT,
-                    "qmatmul: QUANTIZE_X needs int4 weights, fp x and y, group scales and no x_scales");
+                    "qmatmul: QUANTIZE_X needs fp x and y, weight scales and no x_scales");
     const bool w4a8 = d->x_dtype == LUX_HIP_I8 || qx;
     const bool no_scale = d->scale_format == LUX_HIP_SCALE_NONE;
     if (!no_scale && (gs <= 0 || K % gs != 0 || gs % 8 != 0))
@@ -525,7 +524,7 @@ LuxBackendError qmatmul_impl(LuxBackendContext* ctx, const LuxHipQMatmulDesc* d,
         return fail(LUX_BACKEND_ERROR_INVALID_ARGUMENT, "qmatmul: GROUP_PARTIALS needs W4A8, I32 out and a group_size");
 
     if (epilogue != LUX_HIP_EPILOGUE_NONE && w4a8)
-        return fail(LUX_BACKEND_ERROR_NOT_SUPPORTED, "qmatmul: epilogues are not fused into the W4A8 kernel");
+        return fail(LUX_BACKEND_ERROR_NOT_SUPPORTED, "qmatmul: epilogues are not fused into the W4A8/W8A8 kernel");
     if (silu_mul && n_out % 2 != 0)
         return fail(LUX_BACKEND_ERROR_INVALID_ARGUMENT, "qmatmul: SILU_MUL needs an even n_out (gate rows, then up rows)");
     const int ny = silu_mul ? n_out / 2 : n_out;  // output columns
@@ -579,8 +578,8 @@ LuxBackendError qmatmul_impl(LuxBackendContext* ctx, const LuxHipQMatmulDesc* d,
             if (!ws) return fail(LUX_BACKEND_ERROR_OUT_OF_MEMORY, "qmatmul: workspace allocation failed");
             a.x = ws;
             a.xs = reinterpret_cast<const float*>(ws + (size_t)M * K);
-            if (d->weight_bits != 4 || !w4a8_supported(a))
-                return fail(LUX_BACKEND_ERROR_NOT_SUPPORTED, "qmatmul: W4A8 shape/format not supported");
+            if (!w4a8_supported(a))
+                return fail(LUX_BACKEND_ERROR_NOT_SUPPORTED, "qmatmul: W4A8/W8A8 shape/format not supported");
             QuantArgs qa{};
             qa.x = X->ptr;
             qa.q = ws;
@@ -595,8 +594,8 @@ LuxBackendError qmatmul_impl(LuxBackendContext* ctx, const LuxHipQMatmulDesc* d,
             if (hipError_t qe = launch_quantize(qa, c->stream); qe != hipSuccess)
                 return end_op(c, qe, "qmatmul (activation quantization)");
         }
-        if (d->weight_bits != 4 || !w4a8_supported(a))
-            return fail(LUX_BACKEND_ERROR_NOT_SUPPORTED, "qmatmul: W4A8 shape/format not supported");
+        if (!w4a8_supported(a))
+            return fail(LUX_BACKEND_ERROR_NOT_SUPPORTED, "qmatmul: W4A8/W8A8 shape/format not supported");
         he = launch_w4a8(a, c->stream);
     } else if (d->weight_bits == 4 && M == 1 && !silu_mul) {
         he = launch_qgemv_i4(a, c->stream);

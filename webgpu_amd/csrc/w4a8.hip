@@ -1,7 +1,9 @@
-// W4A8: int4 weights x int8 activations on the int8 MFMA, exact int32 sums.
+// W4A8 / W8A8: int4 or int8 weights x int8 activations on the int8 MFMA, exact int32 sums.
 //
 // Reference: matmul_int4_int8 (quantized.wgsl:590-647): out[r, c] = sum_k w4(r, k) *
-// a8(k, c) in i32, two's-complement nibbles (unpack_int4x8, quantized.wgsl:148-156).
+// a8(k, c) in i32, two's-complement nibbles (unpack_int4x8, quantized.wgsl:148-156);
+// matmul_int8 (quantized.wgsl:497-555): the same with int8 weights (unpack_int8x4,
+// :167-178).  int8 weights skip the nibble decode and keep the natural k order.
 // Config 5 of BASELINE.json adds group scales: W 11008 x 4096 int4 g128 (fp16
 // scales), A 256 x 4096 int8 with per-token scales; int32 partial sums per group,
 // then y = a_scale[m] * sum_g s[n, g] * P_g[m, n].
@@ -73,7 +75,7 @@ __device__ __forceinline__ u32x4 perm16(u32x4 v) {
 
 // MODE 0: full-K int32; 1: per-group int32 partials; 2: scaled fp output.
 // ONEG: group size == 128, every stage is one whole group (no carry across stages).
-template <int MODE, bool ONEG, ScaleKind SK, YKind YK>
+template <int WB, int MODE, bool ONEG, ScaleKind SK, YKind YK>
 __global__ __launch_bounds__(256, MODE == 1 ? 2 : 3) void k_w4a8(const uint8_t* __restrict__ W,
                                               const void* __restrict__ S,
                                               const int8_t* __restrict__ A,
@@ -97,30 +99,38 @@ __global__ __launch_bounds__(256, MODE == 1 ? 2 : 3) void k_w4a8(const uint8_t* 
     // moves a uniform offset (soffset, scalar arithmetic only).  Reads past the end of
     // a buffer return zeros, so rows >= N and tokens >= M need no clamping (their
     // results are never stored); prefetches past the last stage read harmless data.
+    // int4: a row is K / 2 bytes and a lane's 32 k are 16 bytes; int8: K bytes and 32.
+    constexpr int LW = WB == 4 ? 1 : 2;  // 16-byte loads per lane, row tile and stage
+    const int rowb = K / 8 * WB;
     const __amdgpu_buffer_rsrc_t rw =
-        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(W), (short)0, (int)((size_t)N * K / 2), 0x00020000);
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(W), (short)0, (int)((size_t)N * rowb), 0x00020000);
     const __amdgpu_buffer_rsrc_t ra =
         __builtin_amdgcn_make_buffer_rsrc(const_cast<int8_t*>(A), (short)0, (int)((size_t)M * K), 0x00020000);
-    const int wv0 = (n0 + r16) * (K / 2) + 16 * q;
+    const int wv0 = (n0 + r16) * rowb + 16 * LW * q;
     // activation chunks of a stage: 64 tokens x 8 chunks of 16 B; thread: token tid / 8
     // and tid / 8 + 32, chunk tid % 8 (8 lanes read one token's 128 contiguous bytes)
     const int tk = tid >> 3, part = tid & 7;
     const int av0 = (tb + tk) * K + 16 * part, av1 = av0 + 32 * K;
 
-    auto ldw = [&](u32x4 (&w)[RT], int st) {
-        const int so = __builtin_amdgcn_readfirstlane(st * (GK / 2));
+    auto ldw = [&](u32x4 (&w)[RT * LW], int st) {
+        const int so = __builtin_amdgcn_readfirstlane(st * (GK / 8 * WB));
 #pragma unroll
         for (int f = 0; f < RT; ++f)
-            w[f] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rw, wv0 + f * 16 * (K / 2), so, 0));
+#pragma unroll
+            for (int h = 0; h < LW; ++h)
+                w[f * LW + h] = __builtin_bit_cast(
+                    u32x4, __builtin_amdgcn_raw_buffer_load_b128(rw, wv0 + f * 16 * rowb + 16 * h, so, 0));
     };
     auto lda = [&](u32x4 (&a)[2], int st) {
         const int so = __builtin_amdgcn_readfirstlane(st * GK);
         a[0] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(ra, av0, so, 0));
         a[1] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(ra, av1, so, 0));
     };
+    // int4 weights decode to (k0 k2 k4 k6 | k1 k3 k5 k7) per 8 k, so the activations are
+    // permuted the same way; int8 weights keep the natural order on both sides.
     auto sta = [&](int buf, const u32x4 (&a)[2]) {
-        *reinterpret_cast<u32x4*>(&as[buf][tk][16 * part]) = perm16(a[0]);
-        *reinterpret_cast<u32x4*>(&as[buf][tk + 32][16 * part]) = perm16(a[1]);
+        *reinterpret_cast<u32x4*>(&as[buf][tk][16 * part]) = WB == 4 ? perm16(a[0]) : a[0];
+        *reinterpret_cast<u32x4*>(&as[buf][tk + 32][16 * part]) = WB == 4 ? perm16(a[1]) : a[1];
     };
 
     i32x4 iacc[RT][4];
@@ -154,7 +164,7 @@ __global__ __launch_bounds__(256, MODE == 1 ? 2 : 3) void k_w4a8(const uint8_t* 
     // PD register sets, the loop unrolled by PD so each set is a fixed set of
     // registers.  Set i: W[i] holds the weights of the stage it serves; A[i] its
     // activations, written to LDS at the end of the previous stage.
-    u32x4 Wr[PD][RT], Ar[PD][2];
+    u32x4 Wr[PD][RT * LW], Ar[PD][2];
 #pragma unroll
     for (int i = 0; i < PD; ++i) {
         ldw(Wr[i], i);
@@ -182,7 +192,7 @@ __global__ __launch_bounds__(256, MODE == 1 ? 2 : 3) void k_w4a8(const uint8_t* 
     sta(0, Ar[0]);
     __syncthreads();
 
-    auto stage = [&](int st, u32x4 (&wc)[RT], u32x4 (&ac)[2], const u32x4 (&an)[2]) {
+    auto stage = [&](int st, u32x4 (&wc)[RT * LW], u32x4 (&ac)[2], const u32x4 (&an)[2]) {
         const int buf = st & 1;
         const int k0 = st * GK;
         const bool gstart = ONEG || k0 % gs == 0, gend = ONEG || (k0 + GK) % gs == 0;
@@ -190,9 +200,16 @@ __global__ __launch_bounds__(256, MODE == 1 ? 2 : 3) void k_w4a8(const uint8_t* 
         uint32_t b8[RT][8];
 #pragma unroll
         for (int f = 0; f < RT; ++f) {
-            const uint32_t ww[4] = {wc[f].x, wc[f].y, wc[f].z, wc[f].w};
+            if constexpr (WB == 4) {
+                const uint32_t ww[4] = {wc[f].x, wc[f].y, wc[f].z, wc[f].w};
 #pragma unroll
-            for (int i = 0; i < 4; ++i) unpack_i4_to_i8(ww[i], tc, b8[f][2 * i], b8[f][2 * i + 1]);
+                for (int i = 0; i < 4; ++i) unpack_i4_to_i8(ww[i], tc, b8[f][2 * i], b8[f][2 * i + 1]);
+            } else {
+                const u32x4 w0 = wc[2 * f], w1 = wc[2 * f + 1];
+                const uint32_t ww[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+#pragma unroll
+                for (int i = 0; i < 8; ++i) b8[f][i] = ww[i];
+            }
         }
         ldw(wc, st + PD);
         lda(ac, st + PD);
@@ -300,11 +317,11 @@ __global__ __launch_bounds__(256, MODE == 1 ? 2 : 3) void k_w4a8(const uint8_t* 
 bool w4a8_supported(const QArgs& a) {
     // groups must hold whole 128-k stages; activations/weights 16-byte aligned
     if (((uintptr_t)a.w & 15u) != 0 || ((uintptr_t)a.x & 15u) != 0) return false;
-    if (a.wbits != 4 || a.x_kind != XKind::I8) return false;
+    if ((a.wbits != 4 && a.wbits != 8) || a.x_kind != XKind::I8) return false;
     if (a.k % GK != 0 || a.group_size % GK != 0) return false;
     // byte offsets of the buffer loads are 31-bit
     const size_t lim = (size_t)1 << 31;
-    if ((size_t)(a.n_out + BR) * a.k / 2 >= lim || (size_t)(a.m + BT) * a.k >= lim) return false;
+    if ((size_t)(a.n_out + BR) * a.k / 8 * a.wbits >= lim || (size_t)(a.m + BT) * a.k >= lim) return false;
     if ((size_t)(a.n_out + BR) * (a.k / a.group_size) * 16 >= lim) return false;
     if (a.y_kind == YKind::I32) return true;  // raw sums or per-group partials: no scales used
     // scaled output: the block's scales are staged in LDS (at most GMAX groups per row)
@@ -313,7 +330,7 @@ bool w4a8_supported(const QArgs& a) {
     return a.scale_kind != ScaleKind::None && a.xs != nullptr && G <= GMAX && BR * G * sb <= 256 * 16 * SCH;
 }
 
-template <int MODE, bool ONEG, ScaleKind SK, YKind YK>
+template <int WB, int MODE, bool ONEG, ScaleKind SK, YKind YK>
 static void launch_g(const QArgs& a, hipStream_t s) {
     const int nrb = (a.n_out + BR - 1) / BR, ntb = (a.m + BT - 1) / BT;
     const int nrb8 = (nrb + NXCD - 1) / NXCD * NXCD;  // row blocks padded to whole XCD rounds
@@ -324,46 +341,50 @@ static void launch_g(const QArgs& a, hipStream_t s) {
     if (smem > 48 * 1024) {
         static bool raised = false;  // once per instantiation
         if (!raised) {
-            (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&k_w4a8<MODE, ONEG, SK, YK>),
+            (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&k_w4a8<WB, MODE, ONEG, SK, YK>),
                                       hipFuncAttributeMaxDynamicSharedMemorySize, BR * GMAX * (int)sizeof(float));
             raised = true;
         }
     }
-    hipLaunchKernelGGL((k_w4a8<MODE, ONEG, SK, YK>), grid, block, smem, s, reinterpret_cast<const uint8_t*>(a.w),
+    hipLaunchKernelGGL((k_w4a8<WB, MODE, ONEG, SK, YK>), grid, block, smem, s, reinterpret_cast<const uint8_t*>(a.w),
                        a.s, reinterpret_cast<const int8_t*>(a.x), a.xs, a.y, a.m, a.n_out, a.k,
                        a.group_size, tc, nrb, ntb,
                        (a.n_out % 4 == 0 && ((uintptr_t)a.y & 15u) == 0) ? 1 : 0);
 }
 
-template <int MODE, ScaleKind SK, YKind YK>
+template <int WB, int MODE, ScaleKind SK, YKind YK>
 static void launch_t(const QArgs& a, hipStream_t s) {
-    if (MODE != 0 && a.group_size == GK) return launch_g<MODE, true, SK, YK>(a, s);
-    return launch_g<MODE, false, SK, YK>(a, s);
+    if (MODE != 0 && a.group_size == GK) return launch_g<WB, MODE, true, SK, YK>(a, s);
+    return launch_g<WB, MODE, false, SK, YK>(a, s);
 }
 
-template <ScaleKind SK>
+template <int WB, ScaleKind SK>
 static bool launch_scaled(const QArgs& a, hipStream_t s) {
     switch (a.y_kind) {
-        case YKind::F32: launch_t<2, SK, YKind::F32>(a, s); return true;
-        case YKind::F16: launch_t<2, SK, YKind::F16>(a, s); return true;
-        case YKind::BF16: launch_t<2, SK, YKind::BF16>(a, s); return true;
+        case YKind::F32: launch_t<WB, 2, SK, YKind::F32>(a, s); return true;
+        case YKind::F16: launch_t<WB, 2, SK, YKind::F16>(a, s); return true;
+        case YKind::BF16: launch_t<WB, 2, SK, YKind::BF16>(a, s); return true;
+        default: return false;
+    }
+}
+
+template <int WB>
+static bool launch_wb(const QArgs& a, hipStream_t s) {
+    if (a.y_kind == YKind::I32) {
+        if (a.group_partials) launch_t<WB, 1, ScaleKind::None, YKind::I32>(a, s);
+        else launch_t<WB, 0, ScaleKind::None, YKind::I32>(a, s);
+        return true;
+    }
+    switch (a.scale_kind) {
+        case ScaleKind::F16: return launch_scaled<WB, ScaleKind::F16>(a, s);
+        case ScaleKind::F32: return launch_scaled<WB, ScaleKind::F32>(a, s);
+        case ScaleKind::GroupScale: return launch_scaled<WB, ScaleKind::GroupScale>(a, s);
         default: return false;
     }
 }
 
 hipError_t launch_w4a8(const QArgs& a, hipStream_t s) {
-    bool ok = true;
-    if (a.y_kind == YKind::I32) {
-        if (a.group_partials) launch_t<1, ScaleKind::None, YKind::I32>(a, s);
-        else launch_t<0, ScaleKind::None, YKind::I32>(a, s);
-    } else {
-        switch (a.scale_kind) {
-            case ScaleKind::F16: ok = launch_scaled<ScaleKind::F16>(a, s); break;
-            case ScaleKind::F32: ok = launch_scaled<ScaleKind::F32>(a, s); break;
-            case ScaleKind::GroupScale: ok = launch_scaled<ScaleKind::GroupScale>(a, s); break;
-            default: ok = false;
-        }
-    }
+    const bool ok = a.wbits == 8 ? launch_wb<8>(a, s) : launch_wb<4>(a, s);
     if (!ok) return hipErrorInvalidValue;
     return hipGetLastError();
 }

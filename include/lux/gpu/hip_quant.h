@@ -30,7 +30,7 @@
 extern "C" {
 #endif
 
-#define LUX_HIP_QUANT_API_VERSION 2u
+#define LUX_HIP_QUANT_API_VERSION 3u
 
 /* Element types.  The first four keep LuxDtype's numbering (docs/api.md:188-197). */
 typedef enum LuxHipDtype {
@@ -163,6 +163,16 @@ typedef struct LuxHipQuantizeDesc {
  * q * s uses the stored scale.  x and q must be 16-byte aligned. */
 LuxBackendError lux_hip_quantize(LuxBackendContext* ctx, const LuxHipQuantizeDesc* desc,
                                  LuxBackendBuffer* x, LuxBackendBuffer* q, LuxBackendBuffer* scales);
+
+/* Dequantizers (no host bridge in the reference): dequantize_nax_int4_sym
+ * (quantized_nax.wgsl:264-282) and dequantize_nax_int8_group, symmetric branch
+ * (:364-386): out[r, k] = f32(q(r, k)) * s(r, k / group_size), computed in fp32 (exact for
+ * fp16 scales) and rounded to nearest-even when x_dtype is F16 or BF16.  The descriptor is
+ * the quantizer's: x_dtype names the output type, group_size a multiple of 8 dividing k,
+ * q and out 16-byte aligned. */
+LuxBackendError lux_hip_dequantize(LuxBackendContext* ctx, const LuxHipQuantizeDesc* desc,
+                                   LuxBackendBuffer* q, LuxBackendBuffer* scales,
+                                   LuxBackendBuffer* out);
 
 /* Re-code `words` packed int4 words between offset-binary (quantized_nax.wgsl:94-112)
  * and two's complement (quantized.wgsl:124-156): every nibble xor 8 (ob = tc ^ 0x8), a

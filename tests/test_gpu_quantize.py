@@ -1,4 +1,4 @@
-"""GPU parity: producers and codecs of the matmul inputs (lux_hip_quantize,
+"""GPU parity: producers and codecs of the matmul inputs (lux_hip_quantize, lux_hip_dequantize,
 lux_hip_convert_nibbles, lux_hip_convert_scales, lux_hip_requantize_i32).
 
 Oracle: compute_group_scales (quantized_nax.wgsl:157-232), quantize_nax_int4_sym
@@ -205,3 +205,70 @@ def test_quantize_rejects(ctx):
             ctx.quantize(W.quant_desc(**kw), xb, qb, sb)
     with pytest.raises(W.LuxError):  # output buffer too small
         ctx.quantize(W.quant_desc(4, 96, 8, 32, 0, W.SCALE_F32, W.F32), xb, ctx.alloc(16), sb)
+
+
+# --------------------------------------------------------------------------- dequantize
+def _scale_buffers(r, rows, groups, sfmt):
+    """Scales in the requested storage and as the f32 values the dequantizer reads."""
+    s32 = r.uniform(0.005, 0.02, size=(rows, groups)).astype(np.float32)
+    if sfmt == W.SCALE_F16:
+        s16 = s32.astype(np.float16)
+        return s16, s16.astype(np.float32)
+    if sfmt == W.SCALE_F32:
+        return s32, s32
+    gsr = np.zeros((rows, groups, 4), np.float32)  # GroupScale {scale, zero_point, min, max}
+    gsr[..., 0], gsr[..., 2], gsr[..., 3] = s32, -1.0, 1.0
+    return gsr, s32
+
+
+@pytest.mark.parametrize("bits,rows,k,gs,coding,sfmt,odt", [
+    (4, 14336, 4096, 32, 0, W.SCALE_F16, "f32"),   # config 2/4 weights, offset-binary
+    (4, 100, 512, 128, 1, W.SCALE_F32, "f16"),     # two's complement nibbles
+    (4, 37, 256, 64, 0, W.SCALE_GROUPSCALE, "bf16"),
+    (8, 2048, 8192, 8192, 0, W.SCALE_F16, "f32"),  # config 3 per-row int8 (a slice of rows)
+    (8, 96, 1024, 64, 0, W.SCALE_F32, "bf16"),
+])
+def test_dequantize_matches_oracle(ctx, bits, rows, k, gs, coding, sfmt, odt):
+    """dequantize_nax_int4_sym / dequantize_nax_int8_group: f32 output bit-exact against
+    the oracle; f16/bf16 output equal to the oracle's f32 rounded to nearest-even."""
+    r = rng(bits * rows + k + gs)
+    sbuf, sf = _scale_buffers(r, rows, k // gs, sfmt)
+    if bits == 4:
+        q = r.integers(-8, 8, size=(rows, k))
+        qb = pack_nibbles(q, coding)
+        ref = oracle.dequantize_int4(qb.reshape(-1), sf.reshape(-1), gs, coding).reshape(rows, k)
+    else:
+        qb = r.integers(-128, 128, size=(rows, k)).astype(np.int8)
+        ref = oracle.dequantize_int8(qb.reshape(-1), sf.reshape(-1), gs).reshape(rows, k)
+    onp = {"f32": np.float32, "f16": np.float16, "bf16": np.uint16}[odt]
+    ob = ctx.alloc(rows * k * np.dtype(onp).itemsize)
+    ctx.dequantize(W.quant_desc(rows, k, bits, gs, coding, sfmt, XD[odt]), ctx.upload(qb), ctx.upload(sbuf), ob)
+    got = ctx.download(ob, onp, (rows, k))
+    if odt == "f32":
+        assert np.array_equal(got.view(np.uint32), ref.astype(np.float32).view(np.uint32))
+    elif odt == "f16":
+        assert np.array_equal(got.view(np.uint16), ref.astype(np.float32).astype(np.float16).view(np.uint16))
+    else:
+        assert np.array_equal(got, bf16_bits(ref.astype(np.float32)))
+
+
+def test_dequantize_roundtrip_and_rejects(ctx):
+    """quantize then dequantize reproduces the input to within half a step of its group's
+    scale (the symmetric grid), and bad descriptors are refused."""
+    r = rng(321)
+    rows, k, gs = 256, 1024, 32
+    x = r.standard_normal((rows, k)).astype(np.float32)
+    d = W.quant_desc(rows, k, 4, gs, 0, W.SCALE_F32, W.F32)
+    qb, sb, ob = ctx.alloc(rows * k // 2), ctx.alloc(rows * (k // gs) * 4), ctx.alloc(rows * k * 4)
+    ctx.quantize(d, ctx.upload(x), qb, sb)
+    ctx.dequantize(d, qb, sb, ob)
+    back = ctx.download(ob, np.float32, (rows, k))
+    s = ctx.download(sb, np.float32, (rows, k // gs))
+    err = np.abs(back - x).reshape(rows, k // gs, gs).max(axis=2)
+    assert np.all(err <= 0.5 * s * (1 + 1e-6))
+    with pytest.raises(W.LuxError):  # group size not a multiple of 8
+        ctx.dequantize(W.quant_desc(rows, k, 4, 12, 0, W.SCALE_F32, W.F32), qb, sb, ob)
+    with pytest.raises(W.LuxError):  # output too small
+        ctx.dequantize(d, qb, sb, ctx.alloc(16))
+    with pytest.raises(W.LuxError):  # an integer output type
+        ctx.dequantize(W.quant_desc(rows, k, 4, gs, 0, W.SCALE_F32, W.I8), qb, sb, ob)

@@ -139,6 +139,7 @@ EXPORTS = {
     "lux_hip_rms_norm": (c_int, [c_void_p, POINTER(RmsNormParams), c_void_p, c_void_p, c_void_p,
                                  c_void_p]),
     "lux_hip_quantize": (c_int, [c_void_p, POINTER(QuantizeDesc), c_void_p, c_void_p, c_void_p]),
+    "lux_hip_dequantize": (c_int, [c_void_p, POINTER(QuantizeDesc), c_void_p, c_void_p, c_void_p]),
     "lux_hip_convert_nibbles": (c_int, [c_void_p, c_void_p, c_void_p, c_size_t, c_int, c_int]),
     "lux_hip_convert_scales": (c_int, [c_void_p, c_void_p, c_int, c_void_p, c_int, c_size_t]),
     "lux_hip_requantize_i32": (c_int, [c_void_p, c_void_p, c_void_p, c_size_t, c_float, c_float,
@@ -380,6 +381,11 @@ class Context:
     def quantize(self, desc: QuantizeDesc, x: Buffer, q: Buffer, scales: Buffer):
         self.plugin.check(self.lib.lux_hip_quantize(self.handle, byref(desc), x.handle, q.handle,
                                                     scales.handle), "quantize")
+
+    def dequantize(self, desc: QuantizeDesc, q: Buffer, scales: Buffer, out: Buffer):
+        """out = q * s; desc.x_dtype is the output type (lux_hip_dequantize)."""
+        self.plugin.check(self.lib.lux_hip_dequantize(self.handle, byref(desc), q.handle,
+                                                      scales.handle, out.handle), "dequantize")
 
     def convert_nibbles(self, src: Buffer, dst: Buffer, words: int, from_coding: int,
                         to_coding: int):

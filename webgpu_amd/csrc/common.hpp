@@ -249,6 +249,8 @@ struct QuantArgs {
     XKind x_kind;
 };
 hipError_t launch_quantize(const QuantArgs& a, hipStream_t s);
+// out [rows x k] (x_kind F32/F16/BF16) = q * s: the inverse of launch_quantize (x unused).
+hipError_t launch_dequantize(const QuantArgs& a, void* out, hipStream_t s);
 // out[i] = in[i] ^ mask over `words` u32 words (nibble re-coding; in == out allowed).
 hipError_t launch_xor_words(const void* in, void* out, size_t words, uint32_t mask, hipStream_t s);
 hipError_t launch_convert_scales(const void* in, ScaleKind ik, void* out, ScaleKind ok, size_t n, hipStream_t s);

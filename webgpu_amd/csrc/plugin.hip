@@ -681,6 +681,49 @@ LUX_EXPORT LuxBackendError lux_hip_quantize(LuxBackendContext* ctx, const LuxHip
     return end_op(c, launch_quantize(a, c->stream), "quantize");
 }
 
+// Dequantizers dequantize_nax_int4_sym / dequantize_nax_int8_group (symmetric branch),
+// quantized_nax.wgsl:264-282,364-386: out = f32(q) * s, then rounded to x_dtype.
+LUX_EXPORT LuxBackendError lux_hip_dequantize(LuxBackendContext* ctx, const LuxHipQuantizeDesc* d,
+                                              LuxBackendBuffer* q, LuxBackendBuffer* scales,
+                                              LuxBackendBuffer* out) {
+    HipCtx* c = C(ctx);
+    if (!c || !d || !q || !scales || !out) return fail(LUX_BACKEND_ERROR_INVALID_ARGUMENT, "dequantize: NULL argument");
+    if (d->struct_size < sizeof(LuxHipQuantizeDesc))
+        return fail(LUX_BACKEND_ERROR_INVALID_ARGUMENT, "dequantize: struct_size %u too small", d->struct_size);
+    const int rows = d->rows, K = d->k, gs = d->group_size;
+    if (rows < 0 || K < 0) return fail(LUX_BACKEND_ERROR_INVALID_ARGUMENT, "dequantize: negative size");
+    if (d->weight_bits != 4 && d->weight_bits != 8)
+        return fail(LUX_BACKEND_ERROR_INVALID_ARGUMENT, "dequantize: weight_bits must be 4 or 8");
+    if (gs < 8 || gs % 8 != 0 || K % gs != 0)
+        return fail(LUX_BACKEND_ERROR_INVALID_ARGUMENT, "dequantize: group_size %d must be a multiple of 8 dividing k", gs);
+    if (d->nibble_coding != LUX_HIP_NIBBLE_OFFSET_BINARY && d->nibble_coding != LUX_HIP_NIBBLE_TWOS_COMPLEMENT)
+        return fail(LUX_BACKEND_ERROR_INVALID_ARGUMENT, "dequantize: bad nibble_coding");
+    if (d->x_dtype != LUX_HIP_F32 && d->x_dtype != LUX_HIP_F16 && d->x_dtype != LUX_HIP_BF16)
+        return fail(LUX_BACKEND_ERROR_NOT_SUPPORTED, "dequantize: output dtype must be F32, F16 or BF16");
+    if (scale_bytes(d->scale_format) == 0)
+        return fail(LUX_BACKEND_ERROR_INVALID_ARGUMENT, "dequantize: bad scale_format");
+    const size_t n = (size_t)rows * K;
+    HipBuf *Q = B(q), *S = B(scales), *X = B(out);
+    if (!fits(Q, n * d->weight_bits / 8) || !fits(X, n * dtype_bytes(d->x_dtype)) ||
+        !fits(S, (size_t)rows * (K / gs) * scale_bytes(d->scale_format)))
+        return fail(LUX_BACKEND_ERROR_INVALID_ARGUMENT, "dequantize: buffer too small");
+    if (((uintptr_t)Q->ptr | (uintptr_t)X->ptr) & 15u)
+        return fail(LUX_BACKEND_ERROR_NOT_SUPPORTED, "dequantize: q and out must be 16-byte aligned");
+    if (LuxBackendError e = begin_op(c, "dequantize")) return e;
+    if (n == 0) return LUX_BACKEND_OK;
+    QuantArgs a{};
+    a.q = Q->ptr;
+    a.s = S->ptr;
+    a.rows = rows;
+    a.k = K;
+    a.group_size = gs;
+    a.bits = d->weight_bits;
+    a.offset_binary = d->nibble_coding == LUX_HIP_NIBBLE_OFFSET_BINARY;
+    a.scale_kind = static_cast<ScaleKind>(d->scale_format);
+    a.x_kind = static_cast<XKind>(d->x_dtype);
+    return end_op(c, launch_dequantize(a, X->ptr, c->stream), "dequantize");
+}
+
 // Nibble re-coding: offset-binary <-> two's complement (each nibble xor 8).
 LUX_EXPORT LuxBackendError lux_hip_convert_nibbles(LuxBackendContext* ctx, LuxBackendBuffer* in,
                                                    LuxBackendBuffer* out, size_t words, int from_coding,

@@ -8,6 +8,9 @@
 //   quantize_nax_int8_group quantized_nax.wgsl:336-362 (NAX_INT8_SYM) q = clamp(round(x / s),
 //                          -128, 127), 4 per u32 (:136-141)
 //   requantize_int32_to_int8 quantized.wgsl:572-580  clamp(round(x * s_in / s_out) + zp)
+//   dequantize_nax_int4_sym quantized_nax.wgsl:264-282 and dequantize_nax_int8_group
+//                          :364-386 (symmetric branch): x = f32(q) * s, exact in fp32 for
+//                          fp16 scales, then rounded (RNE) to the requested output type
 // The reference runs the scale pass and the quantize pass as two dispatches over a
 // flat tensor, with groups along the flat index; here one kernel does both for a
 // [rows x k] tensor whose groups run along k (the same grouping when group_size
@@ -271,6 +274,40 @@ __global__ __launch_bounds__(256) void k_requantize(const int32_t* __restrict__ 
 
 // ---------------------------------------------------------------------------- host
 
+// Dequantizer: a thread turns 8 consecutive weights (one int4 word or two int8 words)
+// into 8 outputs with one scale (group_size % 8 == 0, so 8 never straddle a group).
+template <int BITS, ScaleKind SK, YKind YK>
+__global__ __launch_bounds__(256) void k_dequantize(const void* __restrict__ Q, const void* __restrict__ S,
+                                                    void* __restrict__ X, size_t chunks, int gpr8,
+                                                    uint32_t ob) {
+    const size_t stride = (size_t)gridDim.x * 256;
+    for (size_t c = (size_t)blockIdx.x * 256 + threadIdx.x; c < chunks; c += stride) {
+        // chunk c covers elements 8c .. 8c+7; its group is 8c / group_size
+        const float sc = scale_from_raw<SK>(load_scale_raw<SK>(S, c / (size_t)gpr8));
+        int q[8];
+        if constexpr (BITS == 4) {
+            const uint32_t w = reinterpret_cast<const uint32_t*>(Q)[c] ^ ob;  // -> offset-binary
+#pragma unroll
+            for (int i = 0; i < 8; ++i) q[i] = (int)((w >> (4 * i)) & 0xFu) - 8;
+        } else {
+            const u32x2 w = reinterpret_cast<const u32x2*>(Q)[c];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                q[i] = (int)(int8_t)(w.x >> (8 * i));
+                q[4 + i] = (int)(int8_t)(w.y >> (8 * i));
+            }
+        }
+        f32x4 lo, hi;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            lo[i] = (float)q[i] * sc;
+            hi[i] = (float)q[4 + i] * sc;
+        }
+        store_y4<YK>(X, 8 * c, lo);
+        store_y4<YK>(X, 8 * c + 4, hi);
+    }
+}
+
 template <XKind XK, int BITS, ScaleKind SK>
 static hipError_t launch_q3(const QuantArgs& a, hipStream_t s) {
     const size_t chunks = (size_t)a.rows * a.k / 8;
@@ -366,6 +403,37 @@ hipError_t launch_requantize(const int32_t* in, int32_t* out, size_t n, float s_
                              hipStream_t s) {
     hipLaunchKernelGGL(k_requantize, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, in, out, n, s_in, s_out, zp);
     return hipGetLastError();
+}
+
+
+template <int BITS, ScaleKind SK>
+static hipError_t launch_dq2(const QuantArgs& a, void* out, hipStream_t s) {
+    const size_t chunks = (size_t)a.rows * a.k / 8;
+    const size_t b = (chunks + 255) / 256;
+    const dim3 grid((unsigned)(b < 16384 ? (b ? b : 1) : 16384)), block(256);
+    const int gpr8 = a.group_size / 8;  // chunks per group
+    const uint32_t ob = a.offset_binary ? 0u : 0x88888888u;
+    switch (a.x_kind) {
+        case XKind::F32: hipLaunchKernelGGL((k_dequantize<BITS, SK, YKind::F32>), grid, block, 0, s, a.q, a.s, out, chunks, gpr8, ob); break;
+        case XKind::F16: hipLaunchKernelGGL((k_dequantize<BITS, SK, YKind::F16>), grid, block, 0, s, a.q, a.s, out, chunks, gpr8, ob); break;
+        case XKind::BF16: hipLaunchKernelGGL((k_dequantize<BITS, SK, YKind::BF16>), grid, block, 0, s, a.q, a.s, out, chunks, gpr8, ob); break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+template <int BITS>
+static hipError_t launch_dq1(const QuantArgs& a, void* out, hipStream_t s) {
+    switch (a.scale_kind) {
+        case ScaleKind::F16: return launch_dq2<BITS, ScaleKind::F16>(a, out, s);
+        case ScaleKind::F32: return launch_dq2<BITS, ScaleKind::F32>(a, out, s);
+        case ScaleKind::GroupScale: return launch_dq2<BITS, ScaleKind::GroupScale>(a, out, s);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+hipError_t launch_dequantize(const QuantArgs& a, void* out, hipStream_t s) {
+    return a.bits == 4 ? launch_dq1<4>(a, out, s) : launch_dq1<8>(a, out, s);
 }
 
 }  // namespace luxhip

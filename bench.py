@@ -260,6 +260,63 @@ def bench_quantize(torch, W, ctx, steps, warmup):
                          "traffic": measured_traffic("quant")}}
 
 
+DQ_BYTES = 14336 * 4096 // 2 + 14336 * (4096 // 32) * 2 + 14336 * 4096 * 4  # int4 + f16 scales in, f32 out
+GB = {"batch": 64, "m": 4096, "n": 128}  # 64 heads x 4096 cached keys x head dim 128
+GB_BYTES = GB["batch"] * (GB["m"] * GB["n"] + GB["n"] + GB["m"]) * 4  # A + x read, y written
+
+
+def bench_dequantize(torch, W, ctx, steps, warmup):
+    """dequantize_nax_int4_sym on config-4 weights: int4 g32 + fp16 scales -> fp32 W
+    [14336 x 4096] (the reference's f32 output)."""
+    from util import int4_weights
+    r = np.random.default_rng(41)
+    _, Wp, sc = int4_weights(r, 14336, 4096, 32)
+    copies = 3
+    qbs = [ctx.upload(Wp) for _ in range(copies)]
+    sbs = [ctx.upload(sc) for _ in range(copies)]
+    ob = ctx.alloc(14336 * 4096 * 4)
+    d = W.quant_desc(14336, 4096, 4, 32, W.NIBBLE_OFFSET_BINARY, W.SCALE_F16, W.F32)
+
+    def launch(i):
+        ctx.dequantize(d, qbs[i % copies], sbs[i % copies], ob)
+
+    n = max(3, min(steps, 30))
+    per = timed_graph(torch, ctx, launch, n, max(1, warmup // 4)) / n
+    for b in qbs + sbs + [ob]:
+        b.free()
+    gbs = DQ_BYTES / per / 1e9
+    return {"us_per_launch": round(per * 1e6, 2), "value": round(gbs, 2), "unit": "GB/s",
+            "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS,
+                         "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
+                         "traffic": measured_traffic("dequant")}}
+
+
+def bench_gemv_batched(torch, W, ctx, steps, warmup):
+    """gemv_batched: 64 fp32 GEMVs of 4096 x 128 (one per head, a decode step's q.K^T over
+    a 4096-token cache), one launch."""
+    r = np.random.default_rng(42)
+    B, M, N = GB["batch"], GB["m"], GB["n"]
+    A = (r.standard_normal(B * M * N) * 0.02).astype(np.float32)
+    x = r.standard_normal(B * N).astype(np.float32)
+    copies = max(2, -(-512 * 2**20 // A.nbytes))
+    abs_ = [ctx.upload(A) for _ in range(copies)]
+    xb, yb = ctx.upload(x), ctx.alloc(B * M * 4)
+
+    def launch(i):
+        ctx.gemv_f32_batched(abs_[i % copies], xb, yb, M, N, B, M * N, N, M)
+
+    n = max(3, min(steps, 100))
+    per = timed_graph(torch, ctx, launch, n, max(1, warmup // 4)) / n
+    for b in abs_ + [xb, yb]:
+        b.free()
+    gbs = GB_BYTES / per / 1e9
+    return {"us_per_launch": round(per * 1e6, 2), "value": round(gbs, 2), "unit": "GB/s",
+            "workload": f"{B} x ({M} x {N}) fp32, strides {M * N}/{N}/{M}",
+            "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS,
+                         "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
+                         "traffic": measured_traffic("gemvb")}}
+
+
 def bench_c5_fp(torch, W, ctx, steps, warmup):
     """Config 5 from fp32 activations: per-token int8 quantization (QUANTIZE_X) + W4A8."""
     from util import int4_weights
@@ -309,7 +366,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=10.0)
-    ap.add_argument("--only", choices=["c1", "c2", "c3", "c4", "c5", "copy", "quant"], default=None,
+    ap.add_argument("--only", choices=["c1", "c2", "c3", "c4", "c5", "copy", "quant", "dequant", "gemvb"],
+                    default=None,
                     help="run one config only (profiling); the JSON line needs both")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -355,6 +413,14 @@ def main():
         qz = bench_quantize(torch, W, ctx, args.steps, args.warmup)
         log(f"  quantize {qz['us_per_launch']} us/launch, {qz['value']} GB/s")
         return
+    if args.only == "dequant":
+        dq = bench_dequantize(torch, W, ctx, args.steps, args.warmup)
+        log(f"  dequantize {dq['us_per_launch']} us/launch, {dq['value']} GB/s")
+        return
+    if args.only == "gemvb":
+        gb = bench_gemv_batched(torch, W, ctx, args.steps, args.warmup)
+        log(f"  gemv_batched {gb['us_per_launch']} us/launch, {gb['value']} GB/s")
+        return
     log("bench: config 2 int4 GEMV")
     c2 = bench_c2(torch, W, ctx, args.steps, args.warmup)
     log(f"  C2 {c2['per_launch_s']*1e6:.2f} us/launch, {c2['gbs']:.1f} GB/s")
@@ -367,7 +433,7 @@ def main():
         log(f"  C4 {c4['per_launch_s']*1e6:.1f} us/launch, {c4['tflops']:.1f} TFLOP/s")
     except W.LuxError as e:
         log(f"  C4 skipped: {e}")
-    c1, c3s, c5, c5f, qz = None, [], None, None, None
+    c1, c3s, c5, c5f, qz, dq, gb = None, [], None, None, None, None, None
     try:
         log("bench: config 1 fp32 GEMV through op_matmul_f32")
         c1 = bench_c1(torch, W, ctx, args.steps, args.warmup)
@@ -385,6 +451,12 @@ def main():
         log("bench: int4 g32 quantizer on config-4 weights (fp32 -> int4 + fp16 scales)")
         qz = bench_quantize(torch, W, ctx, args.steps, args.warmup)
         log(f"  quantize {qz['us_per_launch']} us/launch, {qz['value']} GB/s")
+        log("bench: int4 g32 dequantizer on config-4 weights (int4 + fp16 scales -> fp32)")
+        dq = bench_dequantize(torch, W, ctx, args.steps, args.warmup)
+        log(f"  dequantize {dq['us_per_launch']} us/launch, {dq['value']} GB/s")
+        log("bench: batched fp32 GEMV, 64 x 4096 x 128")
+        gb = bench_gemv_batched(torch, W, ctx, args.steps, args.warmup)
+        log(f"  gemv_batched {gb['us_per_launch']} us/launch, {gb['value']} GB/s")
     except W.LuxError as e:
         log(f"  C1/C3/C5 skipped: {e}")
     cpu = None
@@ -427,6 +499,8 @@ def main():
         "w4a8_gemm_c5": c5,
         "w4a8_c5_from_fp32_activations": c5f,
         "quantize_int4_g32_c4_weights": qz,
+        "dequantize_int4_g32_c4_weights": dq,
+        "gemv_f32_batched": gb,
     }
     print(json.dumps(out), flush=True)
     ctx.close()

@@ -236,6 +236,31 @@ LuxBackendError lux_hip_gemv_f32(LuxBackendContext* ctx, LuxBackendBuffer* a,
                                  LuxBackendBuffer* x, LuxBackendBuffer* y,
                                  const LuxHipGemvParams* params);
 
+/* BatchGemvParams of gemv.wgsl:280-293: batch_count independent row GEMVs. */
+typedef struct LuxHipGemvBatchedParams {
+    uint32_t M;           /* rows of each A                          */
+    uint32_t N;           /* columns of each A                       */
+    float alpha;
+    float beta;           /* y is read only when beta != 0           */
+    uint32_t lda;         /* leading dimension of each A (>= N)      */
+    uint32_t batch_count;
+    uint32_t stride_a;    /* elements between consecutive matrices   */
+    uint32_t stride_x;    /* elements between consecutive x vectors  */
+    uint32_t stride_y;    /* elements between consecutive y vectors (>= M when batch_count > 1) */
+    uint32_t _pad0;
+    uint32_t _pad1;
+    uint32_t _pad2;
+} LuxHipGemvBatchedParams;
+
+/* Batched fp32 GEMV, replaces gemv_batched (gemv.wgsl:297-354): for each batch b,
+ * y_b[M] = alpha * A_b x_b + beta * y_b with A_b = a + b*stride_a (row-major, lda),
+ * x_b = x + b*stride_x, y_b = y + b*stride_y.  stride_a or stride_x may be 0 (one
+ * matrix or one vector shared by all batches); y vectors may not overlap, so
+ * stride_y < M with batch_count > 1 is refused (the WGSL would race on y). */
+LuxBackendError lux_hip_gemv_f32_batched(LuxBackendContext* ctx, LuxBackendBuffer* a,
+                                         LuxBackendBuffer* x, LuxBackendBuffer* y,
+                                         const LuxHipGemvBatchedParams* params);
+
 /* fp16 GEMV with fp32 accumulation: y[M] (f32) = A[M x N] (f16) . x[N] (f16).
  * Replaces dot_product_fp16_fp32 (fp_quantized.wgsl:418-469) used with one shared
  * vector.  lda in elements, even. */

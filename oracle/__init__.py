@@ -46,6 +46,8 @@ _SIGS = {
     "lo_matmul_f32": (None, [_P, _P, _P, _I, _I, _I]),
     "lo_gemv_row_parallel": (None, [_P, _P, _P, _I, _I, _I, _F, _F]),
     "lo_gemv_transpose": (None, [_P, _P, _P, _I, _I, _I, _F, _F]),
+    "lo_gemv_batched": (None, [_P, _P, _P, _I, _I, _I, _F, _F, _I, ctypes.c_long, ctypes.c_long,
+                               ctypes.c_long]),
     "lo_gemv_vec4": (None, [_P, _P, _P, _I, _I, _I, _F, _F]),
     "lo_gemv_f16_f32": (None, [_P, _P, _P, _I, _I, _I]),
     "lo_matmul_nax_grouped": (None, [_P, _P, _P, _P, _I, _I, _I, _I, _I]),
@@ -192,6 +194,21 @@ def gemv_row_parallel(A, x, y=None, alpha=1.0, beta=0.0, lda=None, rows=None, co
 
 def gemv_transpose(A, x, y=None, alpha=1.0, beta=0.0):
     return _gemv("lo_gemv_transpose", A, x, y, alpha, beta)
+
+
+def gemv_batched(A, x, y, M, N, batch, stride_a, stride_x, stride_y, alpha=1.0, beta=0.0,
+                 lda=None):
+    """gemv_batched over flat buffers A, x, y (strides and lda in elements); returns the new y."""
+    A = _c(A, np.float32).reshape(-1)
+    x = _c(x, np.float32).reshape(-1)
+    y = _c(y, np.float32).reshape(-1).copy()
+    lda = N if lda is None else lda
+    if batch > 0 and M > 0:
+        assert A.size >= (batch - 1) * stride_a + (M - 1) * lda + N
+        assert x.size >= (batch - 1) * stride_x + N and y.size >= (batch - 1) * stride_y + M
+    lib().lo_gemv_batched(_p(A), _p(x), _p(y), M, N, lda, float(alpha), float(beta), batch,
+                          stride_a, stride_x, stride_y)
+    return y
 
 
 def gemv_vec4(A, x, y=None, alpha=1.0, beta=0.0):

@@ -251,6 +251,17 @@ void lo_gemv_row_parallel(const float* A, const float* x, float* y, int M, int N
     }
 }
 
+/* gemv.wgsl:297-354 (gemv_batched): workgroup b*M + row computes row `row` of batch b with
+ * the row_parallel reduction, over A + b*stride_a, x + b*stride_x, y + b*stride_y.
+ * Strides and lda are in elements, as the u32 fields of BatchGemvParams. */
+void lo_gemv_batched(const float* A, const float* x, float* y, int M, int N, int lda,
+                     float alpha, float beta, int batch, long stride_a, long stride_x,
+                     long stride_y) {
+    for (int b = 0; b < batch; ++b)
+        lo_gemv_row_parallel(A + (size_t)b * stride_a, x + (size_t)b * stride_x,
+                             y + (size_t)b * stride_y, M, N, lda, alpha, beta);
+}
+
 /* gemv.wgsl:103-149 */
 void lo_gemv_transpose(const float* A, const float* x, float* y, int M, int N, int lda,
                        float alpha, float beta) {

@@ -1,7 +1,7 @@
 """GPU parity: fp32 / fp16 GEMV and op_matmul_f32 through the plugin's C-ABI.
 
-Oracle: gemv_row_parallel / gemv_transpose / WGSL_MATMUL restated in oracle/
-(gemv.wgsl:49-149, src/webgpu_plugin.cpp:138-205).  Config 1 of BASELINE.json is
+Oracle: gemv_row_parallel / gemv_transpose / gemv_batched / WGSL_MATMUL restated in oracle/
+(gemv.wgsl:49-149,297-354, src/webgpu_plugin.cpp:138-205).  Config 1 of BASELINE.json is
 the 4096 x 4096 case; the rest are ragged shapes and the alpha/beta/lda paths.
 """
 import numpy as np
@@ -66,6 +66,20 @@ def test_gemv_f32_lda_and_transpose(ctx):
     compare(ctx.download(yb2, np.float32, N), ref2, "gemv_transpose", rel_tol=1e-5)
 
 
+@pytest.mark.parametrize("M,N,lda", [(33, 2047, 2052), (1, 1024, 1024), (8192, 1030, 1032)])
+def test_gemv_f32_rows_split_between_waves(ctx, M, N, lda):
+    """Few long rows: each row's two halves go to two waves (16-B aligned split, K % 4 tail
+    in the second half); odd M leaves one wave pair of the last block idle."""
+    r = rng(M + N)
+    A = r.standard_normal((M, lda)).astype(np.float32)
+    x = r.standard_normal(N).astype(np.float32)
+    y0 = r.standard_normal(M).astype(np.float32)
+    ref = oracle.gemv_row_parallel(A, x, y0, 0.75, -0.5, lda=lda, rows=M, cols=N)
+    a, xb, yb = ctx.upload(A), ctx.upload(x), ctx.upload(y0)
+    ctx.gemv_f32(a, xb, yb, M, N, 0.75, -0.5, lda=lda)
+    compare(ctx.download(yb, np.float32, M), ref, f"gemv split {M}x{N}", rel_tol=1e-5)
+
+
 @pytest.mark.parametrize("M,K,N", [(64, 64, 64), (100, 37, 70), (1, 512, 300), (257, 129, 3),
                                    (512, 1024, 256)])
 def test_matmul_f32_general(ctx, M, K, N):
@@ -99,3 +113,70 @@ def test_gemv_f16(ctx, M, K):
     a, xb, yb = ctx.upload(A), ctx.upload(x), ctx.alloc(M * 4)
     ctx.gemv_f16(a, xb, yb, M, K)
     compare(ctx.download(yb, np.float32, M), ref, f"gemv_f16 {M}x{K}", rel_tol=1e-5)
+
+
+# --------------------------------------------------------------------------- gemv_batched
+@pytest.mark.parametrize("B,M,N,lda,pad_a,pad_x,pad_y", [
+    (32, 2048, 128, 128, 0, 0, 0),    # 32 heads x 2048 keys x head dim 128, vector path
+    (5, 13, 301, 307, 11, 3, 2),      # ragged: odd strides take the scalar path
+    (70000, 3, 8, 8, 0, 0, 0),        # more batches than one grid dimension holds
+    (3, 1000, 64, 64, 0, 0, 0),       # short rows, 4 per wave
+    (4, 77, 37, 40, 8, 3, 1),         # short rows with a K % 4 tail and ragged rows
+    (2, 5000, 100, 100, 0, 0, 0),     # short rows, 25 of 32 lanes per row busy
+    (2, 999, 7, 8, 4, 1, 0),          # shortest rows: 8 per wave
+])
+def test_gemv_f32_batched(ctx, B, M, N, lda, pad_a, pad_x, pad_y):
+    """gemv_batched vs the oracle (gemv.wgsl:297-354), rel-L2 <= 1e-5 (fp32, reassociated
+    sums); elements between the y vectors are left untouched."""
+    r = rng(B + M + N)
+    sa, sx, sy = M * lda + pad_a, N + pad_x, M + pad_y
+    A = r.standard_normal((B - 1) * sa + M * lda).astype(np.float32)
+    x = r.standard_normal((B - 1) * sx + N).astype(np.float32)
+    y0 = r.standard_normal((B - 1) * sy + M).astype(np.float32)
+    alpha, beta = (0.5, 2.0) if pad_y else (1.0, 0.0)
+    ref = oracle.gemv_batched(A, x, y0, M, N, B, sa, sx, sy, alpha, beta, lda=lda)
+    a, xb, yb = ctx.upload(A), ctx.upload(x), ctx.upload(y0)
+    ctx.gemv_f32_batched(a, xb, yb, M, N, B, sa, sx, sy, alpha, beta, lda=lda)
+    got = ctx.download(yb, np.float32, y0.size)
+    compare(got, ref, f"gemv_batched {B}x{M}x{N}", rel_tol=1e-5)
+    gaps = np.ones(y0.size, bool)
+    for b in range(B):
+        gaps[b * sy:b * sy + M] = False
+    assert np.array_equal(got[gaps], y0[gaps])
+
+
+def test_gemv_f32_batched_shared_operands_and_errors(ctx):
+    """stride 0 shares one matrix (or one vector) across batches; integer inputs make the
+    result exact.  Overlapping y vectors, short buffers and empty batches."""
+    r = rng(77)
+    B, M, N = 6, 40, 520
+    A = r.integers(-4, 5, size=M * N).astype(np.float32)
+    x = r.integers(-4, 5, size=B * N).astype(np.float32)
+    a, xb, yb = ctx.upload(A), ctx.upload(x), ctx.alloc(B * M * 4)
+    ctx.gemv_f32_batched(a, xb, yb, M, N, B, 0, N, M)            # one A, B vectors
+    want = (x.reshape(B, N).astype(np.int64) @ A.reshape(M, N).T.astype(np.int64)).astype(np.float32)
+    assert np.array_equal(ctx.download(yb, np.float32, (B, M)), want)
+    A2 = r.integers(-4, 5, size=B * M * N).astype(np.float32)
+    a2 = ctx.upload(A2)
+    ctx.gemv_f32_batched(a2, xb, yb, M, N, B, M * N, 0, M)       # B matrices, one x
+    want2 = (A2.reshape(B, M, N).astype(np.int64) @ x[:N].astype(np.int64)).astype(np.float32)
+    assert np.array_equal(ctx.download(yb, np.float32, (B, M)), want2)
+    with pytest.raises(W.LuxError):  # y vectors overlap
+        ctx.gemv_f32_batched(a2, xb, yb, M, N, B, M * N, N, M - 1)
+    with pytest.raises(W.LuxError):  # A holds B-1 matrices only
+        ctx.gemv_f32_batched(a, xb, yb, M, N, B, M * N, N, M)
+    ctx.gemv_f32_batched(a, xb, yb, M, N, 0, 0, 0, 0)            # empty batch: no-op
+    assert np.array_equal(ctx.download(yb, np.float32, (B, M)), want2)
+
+
+def test_gemv_f32_more_rows_than_one_grid_pass(ctx):
+    """2^22 + 37 rows: beyond 2^20 blocks of 4 rows, waves stride over the rest.  Small
+    integers make every row exact, so numpy's int64 product is the check."""
+    r = rng(78)
+    M, N = (1 << 22) + 37, 4
+    A = r.integers(-4, 5, size=(M, N)).astype(np.float32)
+    x = r.integers(-4, 5, size=N).astype(np.float32)
+    a, xb, yb = ctx.upload(A), ctx.upload(x), ctx.alloc(M * 4)
+    ctx.gemv_f32(a, xb, yb, M, N)
+    want = (A.astype(np.int64) @ x.astype(np.int64)).astype(np.float32)
+    assert np.array_equal(ctx.download(yb, np.float32, M), want)

@@ -227,6 +227,8 @@ def _scale_buffers(r, rows, groups, sfmt):
     (4, 37, 256, 64, 0, W.SCALE_GROUPSCALE, "bf16"),
     (8, 2048, 8192, 8192, 0, W.SCALE_F16, "f32"),  # config 3 per-row int8 (a slice of rows)
     (8, 96, 1024, 64, 0, W.SCALE_F32, "bf16"),
+    (4, 50, 960, 96, 1, W.SCALE_F16, "f32"),       # 12 chunks per group: not a power of two
+    (8, 20, 720, 24, 0, W.SCALE_F32, "f16"),
 ])
 def test_dequantize_matches_oracle(ctx, bits, rows, k, gs, coding, sfmt, odt):
     """dequantize_nax_int4_sym / dequantize_nax_int8_group: f32 output bit-exact against

@@ -146,6 +146,29 @@ def test_gemv_exact_and_alpha_beta(fn):
     assert np.array_equal(getattr(O, fn)(Ar, e), Ar[:, 517])
 
 
+def test_gemv_batched_pinned():
+    """gemv_batched: exact on small integers (closed form per batch), batch b equal to
+    gemv_row_parallel on its own slice, and stride 0 for A or x shares one operand."""
+    r = rng(31)
+    B, M, N, lda = 5, 13, 301, 307
+    sa, sx, sy = M * lda + 11, N + 3, M + 2
+    A = r.integers(-4, 5, size=(B - 1) * sa + M * lda).astype(np.float32)
+    x = r.integers(-4, 5, size=(B - 1) * sx + N).astype(np.float32)
+    y0 = r.integers(-4, 5, size=(B - 1) * sy + M).astype(np.float32)
+    got = O.gemv_batched(A, x, y0, M, N, B, sa, sx, sy, alpha=2.0, beta=-1.0, lda=lda)
+    want = y0.copy()  # gaps between the y vectors stay untouched
+    for b in range(B):
+        Ab = A[b * sa:b * sa + M * lda].reshape(M, lda)[:, :N].astype(np.int64)
+        xb = x[b * sx:b * sx + N].astype(np.int64)
+        want[b * sy:b * sy + M] = (2 * (Ab @ xb) - y0[b * sy:b * sy + M].astype(np.int64)).astype(np.float32)
+    assert np.array_equal(got, want)
+    Ar = r.standard_normal(M * N).astype(np.float32)
+    xr = r.standard_normal(B * N).astype(np.float32)
+    got = O.gemv_batched(Ar, xr, np.zeros(B * M, np.float32), M, N, B, 0, N, M)
+    for b in range(B):
+        assert np.array_equal(got[b * M:(b + 1) * M], O.gemv_row_parallel(Ar.reshape(M, N), xr[b * N:(b + 1) * N]))
+
+
 def test_gemv_transpose_and_fp16():
     r = rng(4)
     A = r.integers(-4, 5, size=(300, 41)).astype(np.float32)

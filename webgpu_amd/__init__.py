@@ -116,6 +116,13 @@ class GemvParams(Structure):
                 ("lda", c_uint32), ("trans", c_uint32), ("_pad0", c_uint32), ("_pad1", c_uint32)]
 
 
+class GemvBatchedParams(Structure):
+    _fields_ = [("M", c_uint32), ("N", c_uint32), ("alpha", c_float), ("beta", c_float),
+                ("lda", c_uint32), ("batch_count", c_uint32), ("stride_a", c_uint32),
+                ("stride_x", c_uint32), ("stride_y", c_uint32), ("_pad0", c_uint32),
+                ("_pad1", c_uint32), ("_pad2", c_uint32)]
+
+
 # Typed views of the vtable slots this plugin fills.
 _T_CREATE = CFUNCTYPE(c_void_p, c_int)
 _T_DESTROY = CFUNCTYPE(None, c_void_p)
@@ -145,6 +152,8 @@ EXPORTS = {
     "lux_hip_requantize_i32": (c_int, [c_void_p, c_void_p, c_void_p, c_size_t, c_float, c_float,
                                        c_int32]),
     "lux_hip_gemv_f32": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, POINTER(GemvParams)]),
+    "lux_hip_gemv_f32_batched": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p,
+                                         POINTER(GemvBatchedParams)]),
     "lux_hip_gemv_f16": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_uint32, c_uint32,
                                  c_uint32]),
     "lux_hip_buffer_wrap": (c_void_p, [c_void_p, c_void_p, c_size_t]),
@@ -350,6 +359,14 @@ class Context:
         p = GemvParams(M, N, alpha, beta, lda if lda is not None else N, int(trans), 0, 0)
         self.plugin.check(self.lib.lux_hip_gemv_f32(self.handle, a.handle, x.handle, y.handle,
                                                     byref(p)), "gemv_f32")
+
+    def gemv_f32_batched(self, a: Buffer, x: Buffer, y: Buffer, M: int, N: int, batch: int,
+                         stride_a: int, stride_x: int, stride_y: int, alpha=1.0, beta=0.0, lda=None):
+        """gemv_batched (gemv.wgsl:297-354); strides and lda in elements."""
+        p = GemvBatchedParams(M, N, alpha, beta, lda if lda is not None else N, batch, stride_a,
+                              stride_x, stride_y, 0, 0, 0)
+        self.plugin.check(self.lib.lux_hip_gemv_f32_batched(self.handle, a.handle, x.handle, y.handle,
+                                                            byref(p)), "gemv_f32_batched")
 
     def gemv_f16(self, a: Buffer, x: Buffer, y: Buffer, M: int, N: int, lda=None):
         self.plugin.check(self.lib.lux_hip_gemv_f16(self.handle, a.handle, x.handle, y.handle, M, N,

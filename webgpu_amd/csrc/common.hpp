@@ -208,6 +208,9 @@ struct QArgs {
 
 hipError_t launch_gemv_f32(const float* A, const float* x, float* y, int M, int K, int lda,
                            float alpha, float beta, hipStream_t s);
+hipError_t launch_gemv_f32_batched(const float* A, const float* x, float* y, int M, int K, int lda,
+                                   float alpha, float beta, int batch, size_t sa, size_t sx,
+                                   size_t sy, hipStream_t s);
 hipError_t launch_gemv_f32_t(const float* A, const float* x, float* y, int M, int N, int lda,
                              float alpha, float beta, hipStream_t s);
 hipError_t launch_gemm_f32(const float* A, const float* B, float* C, int M, int K, int N,

@@ -468,6 +468,34 @@ LUX_EXPORT LuxBackendError lux_hip_gemv_f32(LuxBackendContext* ctx, LuxBackendBu
     return end_op(c, he, "gemv_f32");
 }
 
+LUX_EXPORT LuxBackendError lux_hip_gemv_f32_batched(LuxBackendContext* ctx, LuxBackendBuffer* a,
+                                                    LuxBackendBuffer* x, LuxBackendBuffer* y,
+                                                    const LuxHipGemvBatchedParams* p) {
+    HipCtx* c = C(ctx);
+    HipBuf *A = B(a), *X = B(x), *Y = B(y);
+    if (!c || !A || !X || !Y || !p)
+        return fail(LUX_BACKEND_ERROR_INVALID_ARGUMENT, "gemv_f32_batched: NULL argument");
+    const size_t M = p->M, N = p->N, lda = p->lda, nb = p->batch_count;
+    const size_t sa = p->stride_a, sx = p->stride_x, sy = p->stride_y;
+    if (lda < N || M > INT32_MAX || N > INT32_MAX || lda > INT32_MAX || nb > INT32_MAX)
+        return fail(LUX_BACKEND_ERROR_INVALID_ARGUMENT, "gemv_f32_batched: lda < N or size too large");
+    if (nb > 1 && M > 0 && sy < M)
+        return fail(LUX_BACKEND_ERROR_INVALID_ARGUMENT,
+                    "gemv_f32_batched: stride_y %zu < M %zu makes the y vectors overlap", sy, M);
+    if (M > 0 && nb > 0) {
+        const size_t a_need = ((nb - 1) * sa + (M - 1) * lda + N) * 4;
+        const size_t x_need = ((nb - 1) * sx + N) * 4, y_need = ((nb - 1) * sy + M) * 4;
+        if (!fits(A, a_need) || !fits(X, x_need) || !fits(Y, y_need))
+            return fail(LUX_BACKEND_ERROR_INVALID_ARGUMENT, "gemv_f32_batched: buffer too small");
+    }
+    if (LuxBackendError e = begin_op(c, "gemv_f32_batched")) return e;
+    if (M == 0 || nb == 0) return LUX_BACKEND_OK;
+    hipError_t he = launch_gemv_f32_batched((const float*)A->ptr, (const float*)X->ptr, (float*)Y->ptr,
+                                            (int)M, (int)N, (int)lda, p->alpha, p->beta, (int)nb, sa, sx,
+                                            sy, c->stream);
+    return end_op(c, he, "gemv_f32_batched");
+}
+
 LUX_EXPORT LuxBackendError lux_hip_gemv_f16(LuxBackendContext* ctx, LuxBackendBuffer* a,
                                             LuxBackendBuffer* x, LuxBackendBuffer* y, uint32_t M,
                                             uint32_t N, uint32_t lda) {

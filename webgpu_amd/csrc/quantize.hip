@@ -274,37 +274,58 @@ __global__ __launch_bounds__(256) void k_requantize(const int32_t* __restrict__ 
 
 // ---------------------------------------------------------------------------- host
 
-// Dequantizer: a thread turns 8 consecutive weights (one int4 word or two int8 words)
-// into 8 outputs with one scale (group_size % 8 == 0, so 8 never straddle a group).
-template <int BITS, ScaleKind SK, YKind YK>
+// Dequantizer, 8-weight chunks (one int4 word or two int8 words; group_size % 8 == 0, so
+// a chunk never straddles a group).  A wave covers 64 chunks per step and lane l takes
+// half (l & 1) of chunk base + 32j + (l >> 1), j = 0, 1: its four outputs are elements
+// 8*base + 256j + 4l .. +3, so every store instruction of the wave writes one contiguous
+// span (1 KB of f32).  The natural layout (a lane's 8 outputs as two 16-B stores 32 B
+// apart) half-fills each span per instruction and ran 1.5x slower (62 us against 40 us
+// for 14336 x 4096 int4 -> f32).  Lane pairs read the same int4 word; int8 words are
+// read contiguously.  One pass of the grid where it fits, grid-stride beyond.
+template <int BITS, ScaleKind SK, YKind YK, bool POW2>
+__device__ __forceinline__ void dequant_pair(const void* __restrict__ Q, const void* __restrict__ S,
+                                             void* __restrict__ X, size_t base, size_t chunks, int gpr8,
+                                             int gshift, uint32_t ob, bool full) {
+    const int lane = threadIdx.x & 63, h = lane & 1;
+    uint32_t w[2] = {0u, 0u};
+    float sc[2] = {0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const size_t c = base + 32 * j + (lane >> 1);
+        if (full || c < chunks) {
+            if constexpr (BITS == 4) w[j] = reinterpret_cast<const uint32_t*>(Q)[c] ^ ob;  // -> offset-binary
+            else w[j] = reinterpret_cast<const uint32_t*>(Q)[2 * c + h];
+            sc[j] = scale_from_raw<SK>(load_scale_raw<SK>(S, POW2 ? c >> gshift : c / (size_t)gpr8));
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const size_t c = base + 32 * j + (lane >> 1);
+        if (!full && c >= chunks) break;
+        f32x4 o;
+        if constexpr (BITS == 4) {
+            const uint32_t v = w[j] >> (16 * h);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) o[i] = (float)((int)((v >> (4 * i)) & 0xFu) - 8) * sc[j];
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) o[i] = (float)(int)(int8_t)(w[j] >> (8 * i)) * sc[j];
+        }
+        store_y4<YK>(X, 8 * base + 256 * j + 4 * lane, o);
+    }
+}
+
+// POW2: group_size / 8 is a power of two and the group index is a shift.  Waves whose
+// 64 chunks are all in range take an unguarded copy of the body, so both word loads
+// issue back to back.
+template <int BITS, ScaleKind SK, YKind YK, bool POW2>
 __global__ __launch_bounds__(256) void k_dequantize(const void* __restrict__ Q, const void* __restrict__ S,
                                                     void* __restrict__ X, size_t chunks, int gpr8,
-                                                    uint32_t ob) {
-    const size_t stride = (size_t)gridDim.x * 256;
-    for (size_t c = (size_t)blockIdx.x * 256 + threadIdx.x; c < chunks; c += stride) {
-        // chunk c covers elements 8c .. 8c+7; its group is 8c / group_size
-        const float sc = scale_from_raw<SK>(load_scale_raw<SK>(S, c / (size_t)gpr8));
-        int q[8];
-        if constexpr (BITS == 4) {
-            const uint32_t w = reinterpret_cast<const uint32_t*>(Q)[c] ^ ob;  // -> offset-binary
-#pragma unroll
-            for (int i = 0; i < 8; ++i) q[i] = (int)((w >> (4 * i)) & 0xFu) - 8;
-        } else {
-            const u32x2 w = reinterpret_cast<const u32x2*>(Q)[c];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                q[i] = (int)(int8_t)(w.x >> (8 * i));
-                q[4 + i] = (int)(int8_t)(w.y >> (8 * i));
-            }
-        }
-        f32x4 lo, hi;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            lo[i] = (float)q[i] * sc;
-            hi[i] = (float)q[4 + i] * sc;
-        }
-        store_y4<YK>(X, 8 * c, lo);
-        store_y4<YK>(X, 8 * c + 4, hi);
+                                                    int gshift, uint32_t ob) {
+    const size_t waves = (size_t)gridDim.x * 4;
+    for (size_t base = ((size_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * 64; base < chunks; base += waves * 64) {
+        if (base + 64 <= chunks) dequant_pair<BITS, SK, YK, POW2>(Q, S, X, base, chunks, gpr8, gshift, ob, true);
+        else dequant_pair<BITS, SK, YK, POW2>(Q, S, X, base, chunks, gpr8, gshift, ob, false);
     }
 }
 
@@ -409,14 +430,17 @@ hipError_t launch_requantize(const int32_t* in, int32_t* out, size_t n, float s_
 template <int BITS, ScaleKind SK>
 static hipError_t launch_dq2(const QuantArgs& a, void* out, hipStream_t s) {
     const size_t chunks = (size_t)a.rows * a.k / 8;
-    const size_t b = (chunks + 255) / 256;
-    const dim3 grid((unsigned)(b < 16384 ? (b ? b : 1) : 16384)), block(256);
+    const size_t b = (chunks + 255) / 256;  // 64 chunks per wave, 4 waves per block
+    const dim3 grid((unsigned)(b < (1u << 22) ? (b ? b : 1) : (1u << 22))), block(256);
     const int gpr8 = a.group_size / 8;  // chunks per group
+    const int gshift = (gpr8 & (gpr8 - 1)) == 0 ? __builtin_ctz((unsigned)gpr8) : -1;
     const uint32_t ob = a.offset_binary ? 0u : 0x88888888u;
+    auto go = [&](auto kern) { hipLaunchKernelGGL(kern, grid, block, 0, s, a.q, a.s, out, chunks, gpr8, gshift, ob); };
+    const bool p2 = gshift >= 0;
     switch (a.x_kind) {
-        case XKind::F32: hipLaunchKernelGGL((k_dequantize<BITS, SK, YKind::F32>), grid, block, 0, s, a.q, a.s, out, chunks, gpr8, ob); break;
-        case XKind::F16: hipLaunchKernelGGL((k_dequantize<BITS, SK, YKind::F16>), grid, block, 0, s, a.q, a.s, out, chunks, gpr8, ob); break;
-        case XKind::BF16: hipLaunchKernelGGL((k_dequantize<BITS, SK, YKind::BF16>), grid, block, 0, s, a.q, a.s, out, chunks, gpr8, ob); break;
+        case XKind::F32: p2 ? go(k_dequantize<BITS, SK, YKind::F32, true>) : go(k_dequantize<BITS, SK, YKind::F32, false>); break;
+        case XKind::F16: p2 ? go(k_dequantize<BITS, SK, YKind::F16, true>) : go(k_dequantize<BITS, SK, YKind::F16, false>); break;
+        case XKind::BF16: p2 ? go(k_dequantize<BITS, SK, YKind::BF16, true>) : go(k_dequantize<BITS, SK, YKind::BF16, false>); break;
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();

@@ -58,7 +58,10 @@ def _run(ctx, x, rows, k, bits, gs, coding, sfmt, xdt):
     (14336, 4096, 32, "f32", W.SCALE_F16),     # config 2/4 weights
     (300, 512, 128, "bf16", W.SCALE_F32),
     (64, 1024, 64, "f16", W.SCALE_GROUPSCALE),
-    (33, 256, 8, "f32", W.SCALE_F16),
+    (33, 256, 8, "f32", W.SCALE_F16),          # 1056 chunks: a partly filled last wave
+    (10, 160, 16, "bf16", W.SCALE_GROUPSCALE),  # 4 lanes per group
+    (24, 768, 256, "f16", W.SCALE_F16),        # a group fills one half of a wave
+    (40, 1024, 512, "f32", W.SCALE_F32),       # a group spans both halves of a wave
     (16, 8192, 1024, "f32", W.SCALE_F32),      # groups longer than 512: one wave each
     (7, 4096, 4096, "bf16", W.SCALE_F16),      # per-row int4
 ])
@@ -91,6 +94,8 @@ def test_quantize_int4_twos_complement(ctx):
 @pytest.mark.parametrize("rows,k,gs,xdt", [(256, 4096, 4096, "f32"),   # config 5 activations
                                            (28672 // 16, 8192, 8192, "f16"),  # config 3 rows
                                            (100, 512, 32, "bf16"),
+                                           (30, 1024, 512, "f32"),
+                                           (11, 88, 8, "f16"),
                                            (9, 16384, 16384, "f32"),   # 8 chunks per thread
                                            (5, 32768, 32768, "bf16")])  # one wave per group
 def test_quantize_int8_matches_oracle(ctx, rows, k, gs, xdt):
@@ -122,6 +127,37 @@ def test_quantize_edge_values(ctx):
     deq = oracle.dequantize_int4(q.reshape(3, k // 8), sraw.reshape(3, k // gs), gs)
     want = [7, 0, 0, 2, -2, 2, -2, 4, -4, 4, -4, 6, -6, 6, -6, 0] * 2
     assert deq[1, gs:].tolist() == want
+
+
+@pytest.mark.parametrize("bits,sfmt", [(4, W.SCALE_F32), (4, W.SCALE_F16), (8, W.SCALE_F32),
+                                       (8, W.SCALE_F16)])
+def test_quantize_near_ties_and_tiny_scales(ctx, bits, sfmt):
+    """Values whose quotient v / s lies within a few ulps of a half-integer (where a
+    reciprocal-multiply would round the other way than the correctly rounded quotient),
+    and groups with subnormal scales or a scale whose reciprocal overflows.  Bit-exact
+    against the oracle, which divides."""
+    r = rng(77 + bits + sfmt)
+    gs, groups = 32, 2048
+    qmax = 7 if bits == 4 else 127
+    amax = r.uniform(0.05, 300.0, groups).astype(np.float32)
+    if sfmt == W.SCALE_F32:
+        amax[-64:] = (10.0 ** r.uniform(-44, -36, 64)).astype(np.float32)  # subnormal / tiny s
+    s = (amax / np.float32(qmax)).astype(np.float32)
+    s = s.astype(np.float16).astype(np.float32) if sfmt == W.SCALE_F16 else s
+    x = np.zeros((groups, gs), np.float32)
+    x[:, 0] = amax
+    n = r.integers(-qmax, qmax, size=(groups, gs - 1))
+    v = ((n + 0.5) * s[:, None]).astype(np.float32)
+    for _ in range(3):  # walk up to 3 ulps either way of (n + 1/2) * s
+        step = r.integers(-1, 2, size=v.shape)
+        v = np.where(step > 0, np.nextafter(v, np.float32(np.inf)),
+                     np.where(step < 0, np.nextafter(v, np.float32(-np.inf)), v)).astype(np.float32)
+    x[:, 1:] = np.clip(v, -amax[:, None], amax[:, None])
+    rows, k = groups // 8, 8 * gs
+    x = x.reshape(rows, k)
+    q, sraw = _run(ctx, x, rows, k, bits, gs, W.NIBBLE_OFFSET_BINARY, sfmt, "f32")
+    so, _, _, _, words = _oracle_quant(x, gs, bits, sfmt)
+    assert np.array_equal(q, words)
 
 
 def test_quantize_roundtrip_through_gemv(ctx):

@@ -105,3 +105,14 @@ def test_epilogue_rejects(ctx):
     d3 = W.qdesc(63, 256, 4, 4, 32, 0, W.SCALE_F16, W.F16, W.F16)
     with pytest.raises(W.LuxError):  # SILU_MUL needs gate and up rows in pairs
         ctx.qmatmul_ex(d3, wb, sb, xb, None, W.EPI_SILU_MUL, None, None, yb)
+
+
+@pytest.mark.parametrize("epi,ydt", [(W.EPI_SILU_MUL, "f32"), (W.EPI_ADD_RESIDUAL, "f32"),
+                                     (W.EPI_GELU, "f16")])
+def test_epilogue_large_m_config4_shape(ctx, epi, ydt):
+    """m = 2048 against 14336 weight rows (7168 SILU_MUL outputs), the grid of config 4
+    (8 x 56 tiles of 256 x 256); K is cut to 256 to keep the oracle quick.  SILU_MUL is
+    checked in f32: in bf16 the output rounding of two compounded operands alone reaches
+    ~1e-3 rel-L2 against the rounded oracle."""
+    got, ref = _case(ctx, rng(400 + epi), 4, 14336, 256, 2048, 32, "bf16", ydt, epi)
+    compare(got, ref, f"config-4-shape epilogue {epi} {ydt}")

@@ -103,15 +103,21 @@ __global__ __launch_bounds__(64 * MAXW) void k_qgemm_small(
     }
 
     // ---- X staging: 16*MT rows x KC k per chunk = 512*MT chunks of 8 elements.  A chunk is
-    // loaded as one 16-byte vector (two for fp32) ahead of the chunk's weight loads -- loads
-    // retire in issue order, so data needed at the LDS write must be issued before the
-    // long-latency weight prefetch -- and written to LDS after the chunk's MFMAs, converted
-    // to fp16 and reordered into the decode order.
+    // loaded as one 16-byte vector (two for fp32) two k-chunks ahead of its use, into one of
+    // two register sets, and written to LDS (converted to fp16, reordered into the decode
+    // order) after the MFMAs of the chunk before it.  The L2 round trip of the X load is
+    // then covered by a whole chunk of work; loaded one chunk ahead, the LDS write waited
+    // for it every chunk (2 % at config 3 m = 32; lab copies without the weight stream
+    // took 23 and 32 us of the 49 and 60).
+    // Three or four m-tiles, and int8 with group scales and two, keep one register set (X
+    // one chunk ahead): a second set does not fit beside their accumulators and scales.
     constexpr int XS = 2 * MT;                 // chunks per thread (blocks have >= 4 waves)
     constexpr int XV = XK == XKind::F32 ? 2 : 1;
+    constexpr bool X2 = MT <= 2 && !(WB == 8 && !PERROW && MT == 2);
     const int xchunks = 16 * MT * (KC / 8);
-    u32x4 xr[XS][XV];
-    auto load_xc = [&](int k0) {
+    u32x4 xrs[X2 ? 2 : 1][XS][XV];
+    auto load_xc = [&](int set, int k0) __attribute__((always_inline)) {
+        u32x4 (&xr)[XS][XV] = xrs[set];
 #pragma unroll
         for (int i = 0; i < XS; ++i) {
             const int c = tid + i * (int)blockDim.x;
@@ -128,7 +134,8 @@ __global__ __launch_bounds__(64 * MAXW) void k_qgemm_small(
             }
         }
     };
-    auto store_xc = [&](int buf) {
+    auto store_xc = [&](int set, int buf) __attribute__((always_inline)) {
+        const u32x4 (&xr)[XS][XV] = xrs[set];
 #pragma unroll
         for (int i = 0; i < XS; ++i) {
             const int c = tid + i * (int)blockDim.x;
@@ -181,7 +188,7 @@ __global__ __launch_bounds__(64 * MAXW) void k_qgemm_small(
     const int nchunks = K / KC;
     u32x4 wq[2][LPC];                          // two chunks of weights in flight
     uint32_t sq[2][LPC][SPLD > 0 ? SPLD : 1];  // their raw scales
-    auto load_w = [&](int slot, int chunk) {
+    auto load_w = [&](int slot, int chunk) __attribute__((always_inline)) {
         chunk = min(chunk, nchunks - 1);
 #pragma unroll
         for (int l = 0; l < LPC; ++l) {
@@ -203,7 +210,7 @@ __global__ __launch_bounds__(64 * MAXW) void k_qgemm_small(
     // before this chunk's MFMAs run: the prefetch distance is two chunks plus the MFMA
     // and X-read time of one.
     constexpr int SPL = WB == 8 ? 2 : 4;       // 32-k steps per load
-    auto chunk = [&](int buf, int slot, int next) {
+    auto chunk = [&](int buf, int slot, int next) __attribute__((always_inline)) {
         f16x8 av[LPC][SPL];
         uint32_t sc[LPC][SPLD > 0 ? SPLD : 1];
 #pragma unroll
@@ -248,23 +255,44 @@ __global__ __launch_bounds__(64 * MAXW) void k_qgemm_small(
                 }
     };
 
-    // Chunks in pairs so the weight-register slots are static; weights run two chunks
-    // ahead of use, X one chunk ahead (registers, then the other LDS buffer).
-    load_xc(0);
-    load_w(0, 0);
-    load_w(1, 1);
-    store_xc(0);
-    __syncthreads();
-    for (int c = 0; c < nchunks; c += 2) {
-        if (c + 1 < nchunks) load_xc((c + 1) * KC);
-        chunk(0, 0, c + 2);
-        if (c + 1 < nchunks) store_xc(1);
+    // Chunks in pairs so the register slots are static; weights and X both run two chunks
+    // ahead of use (X register set c % 2, then LDS buffer c % 2).
+    if constexpr (X2) {
+        load_xc(0, 0);
+        if (nchunks > 1) load_xc(X2 ? 1 : 0, KC);
+        load_w(0, 0);
+        load_w(1, 1);
+        store_xc(0, 0);
         __syncthreads();
-        if (c + 1 < nchunks) {
-            if (c + 2 < nchunks) load_xc((c + 2) * KC);
-            chunk(1, 1, c + 3);
-            if (c + 2 < nchunks) store_xc(0);
+        for (int c = 0; c < nchunks; c += 2) {
+            if (c + 2 < nchunks) load_xc(0, (c + 2) * KC);
+            chunk(0, 0, c + 2);
+            if (c + 1 < nchunks) store_xc(X2 ? 1 : 0, 1);
             __syncthreads();
+            if (c + 1 < nchunks) {
+                if (c + 3 < nchunks) load_xc(X2 ? 1 : 0, (c + 3) * KC);
+                chunk(1, 1, c + 3);
+                if (c + 2 < nchunks) store_xc(0, 0);
+                __syncthreads();
+            }
+        }
+    } else {  // X one chunk ahead, one register set
+        load_xc(0, 0);
+        load_w(0, 0);
+        load_w(1, 1);
+        store_xc(0, 0);
+        __syncthreads();
+        for (int c = 0; c < nchunks; c += 2) {
+            if (c + 1 < nchunks) load_xc(0, (c + 1) * KC);
+            chunk(0, 0, c + 2);
+            if (c + 1 < nchunks) store_xc(0, 1);
+            __syncthreads();
+            if (c + 1 < nchunks) {
+                if (c + 2 < nchunks) load_xc(0, (c + 2) * KC);
+                chunk(1, 1, c + 3);
+                if (c + 2 < nchunks) store_xc(0, 0);
+                __syncthreads();
+            }
         }
     }
 

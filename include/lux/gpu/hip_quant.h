@@ -268,6 +268,21 @@ LuxBackendError lux_hip_gemv_f16(LuxBackendContext* ctx, LuxBackendBuffer* a,
                                  LuxBackendBuffer* x, LuxBackendBuffer* y, uint32_t M,
                                  uint32_t N, uint32_t lda);
 
+/* DotParams of fp_quantized.wgsl:404-409. */
+typedef struct LuxHipDotParams {
+    uint32_t size;          /* elements per vector                                    */
+    uint32_t num_vectors;
+    uint32_t vector_stride; /* elements between consecutive vectors' starts           */
+    uint32_t _pad;
+} LuxHipDotParams;
+
+/* Batched fp16 dot product with fp32 accumulation, replaces dot_product_fp16_fp32
+ * (fp_quantized.wgsl:418-469), bindings 0..3 = a, b, result, params: result[v] (f32) =
+ * sum_j a[e + j] * b[e + j] over j < size, e = 2 * floor(v * vector_stride / 2) (the WGSL
+ * reads f16 pairs from u32 word base / 2, so an odd base starts one element early). */
+LuxBackendError lux_hip_dot_f16(LuxBackendContext* ctx, LuxBackendBuffer* a, LuxBackendBuffer* b,
+                                LuxBackendBuffer* result, const LuxHipDotParams* params);
+
 /* ---- buffer / stream plumbing (no reference counterpart: the WebGPU plugin
  * hides device addresses, src/webgpu_plugin.cpp:1564) ------------------------ */
 

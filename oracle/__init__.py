@@ -50,6 +50,7 @@ _SIGS = {
                                ctypes.c_long]),
     "lo_gemv_vec4": (None, [_P, _P, _P, _I, _I, _I, _F, _F]),
     "lo_gemv_f16_f32": (None, [_P, _P, _P, _I, _I, _I]),
+    "lo_dot_product_fp16_fp32": (None, [_P, _P, _P, _I, _I, _I]),
     "lo_matmul_nax_grouped": (None, [_P, _P, _P, _P, _I, _I, _I, _I, _I]),
     "lo_dequantize_nax_int4_sym": (None, [_P, _P, _P, _SZ, _I, _I]),
     "lo_dequantize_nax_int8_group": (None, [_P, _P, _P, _SZ, _I]),
@@ -222,6 +223,18 @@ def gemv_f16_f32(A_bits, x_bits) -> np.ndarray:
     y = np.empty(M, np.float32)
     lib().lo_gemv_f16_f32(_p(A), _p(x), _p(y), M, N, N)
     return y
+
+
+def dot_product_fp16_fp32(a_bits, b_bits, size, num_vectors, stride) -> np.ndarray:
+    """dot_product_fp16_fp32 over flat f16 bit arrays (stride in elements)."""
+    a = _c(a_bits, np.uint16).reshape(-1)
+    b = _c(b_bits, np.uint16).reshape(-1)
+    if num_vectors > 0:
+        need = 2 * (((num_vectors - 1) * stride) // 2) + size  # elements read
+        assert a.size >= need and b.size >= need
+    out = np.empty(num_vectors, np.float32)
+    lib().lo_dot_product_fp16_fp32(_p(a), _p(b), _p(out), size, num_vectors, stride)
+    return out
 
 
 # --------------------------------------------------------------------------- grouped

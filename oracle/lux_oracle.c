@@ -304,6 +304,30 @@ void lo_gemv_vec4(const float* A, const float* x, float* y, int M, int N, int ld
     }
 }
 
+/* fp_quantized.wgsl:418-469 as written (dot_product_fp16_fp32): vector v reads the f16
+ * pairs of words base/2 + i, base = v*stride, of both a and b (an odd base starts one
+ * element early), i < ceil(size/2); the second element of the last pair counts only when
+ * size is even.  Strided partials over 256 threads, then the tree. */
+void lo_dot_product_fp16_fp32(const uint16_t* a, const uint16_t* b, float* out, int size,
+                              int num_vectors, int stride) {
+    const int npairs = (size + 1) / 2;
+#pragma omp parallel for schedule(static)
+    for (int v = 0; v < num_vectors; ++v) {
+        const size_t w0 = ((size_t)v * (size_t)stride) / 2;  /* first u32 word */
+        float sh[WG];
+        for (int t = 0; t < WG; ++t) {
+            float s = 0.0f;
+            for (int i = t; i < npairs; i += WG) {
+                const size_t e = 2 * (w0 + i);
+                s = s + lo_f16_to_f32(a[e]) * lo_f16_to_f32(b[e]);
+                if (2 * i + 1 < size) s = s + lo_f16_to_f32(a[e + 1]) * lo_f16_to_f32(b[e + 1]);
+            }
+            sh[t] = s;
+        }
+        out[v] = tree256(sh);
+    }
+}
+
 /* fp_quantized.wgsl:418-469 with the row base r*lda and a shared x. */
 void lo_gemv_f16_f32(const uint16_t* A, const uint16_t* x, float* y, int M, int N, int lda) {
     int npairs = (N + 1) / 2;

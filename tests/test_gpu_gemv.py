@@ -180,3 +180,27 @@ def test_gemv_f32_more_rows_than_one_grid_pass(ctx):
     ctx.gemv_f32(a, xb, yb, M, N)
     want = (A.astype(np.int64) @ x.astype(np.int64)).astype(np.float32)
     assert np.array_equal(ctx.download(yb, np.float32, M), want)
+
+
+@pytest.mark.parametrize("size,nv,stride", [(4096, 512, 4096),   # vector path
+                                            (301, 9, 306),       # odd size, scalar path
+                                            (301, 9, 305),       # odd stride: odd vectors start early
+                                            (64, 3, 0),          # stride 0: one pair of vectors
+                                            (0, 4, 8)])          # empty vectors: zeros
+def test_dot_f16(ctx, size, nv, stride):
+    """dot_product_fp16_fp32 (fp_quantized.wgsl:418-469) vs the oracle; rel-L2 <= 1e-5
+    (exact fp16 products, fp32 sums reassociated)."""
+    r = rng(size + nv + stride)
+    n = max(2 * (((nv - 1) * stride) // 2) + size, 1)
+    a = r.standard_normal(n).astype(np.float16)
+    b = r.standard_normal(n).astype(np.float16)
+    ref = oracle.dot_product_fp16_fp32(a.view(np.uint16), b.view(np.uint16), size, nv, stride)
+    ab, bb, rb = ctx.upload(a), ctx.upload(b), ctx.alloc(nv * 4)
+    ctx.dot_f16(ab, bb, rb, size, nv, stride)
+    got = ctx.download(rb, np.float32, nv)
+    if size == 0:
+        assert np.array_equal(got, np.zeros(nv, np.float32))
+    else:
+        compare(got, ref, f"dot_f16 {size}x{nv}/{stride}", rel_tol=1e-5)
+    with pytest.raises(W.LuxError):  # b one element short
+        ctx.dot_f16(ab, ctx.upload(b[:n - 1]) if n > 1 else ctx.alloc(0), rb, size + 1, nv, stride)

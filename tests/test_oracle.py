@@ -169,6 +169,31 @@ def test_gemv_batched_pinned():
         assert np.array_equal(got[b * M:(b + 1) * M], O.gemv_row_parallel(Ar.reshape(M, N), xr[b * N:(b + 1) * N]))
 
 
+def test_dot_product_fp16_pinned():
+    """dot_product_fp16_fp32: small integers are exact, so each vector's result is the int64
+    dot product of its pairs; an odd size drops the last pair's second element; an odd
+    stride starts odd vectors one element early (word base / 2); one vector per row of a
+    matrix with x repeated equals the shared-x GEMV restatement."""
+    r = rng(41)
+    size, nv, stride = 301, 9, 306
+    n = (nv - 1) * stride + 302
+    a = r.integers(-6, 7, n).astype(np.float16)
+    b = r.integers(-6, 7, n).astype(np.float16)
+    got = O.dot_product_fp16_fp32(a.view(np.uint16), b.view(np.uint16), size, nv, stride)
+    ai, bi = a.astype(np.int64), b.astype(np.int64)
+    want = [int(ai[v * stride:v * stride + size] @ bi[v * stride:v * stride + size]) for v in range(nv)]
+    assert np.array_equal(got, np.array(want, np.float32))
+    stride = 305  # odd: vector v starts at element 2 * (v * 305 // 2)
+    got = O.dot_product_fp16_fp32(a.view(np.uint16), b.view(np.uint16), size, nv, stride)
+    st = [2 * (v * stride // 2) for v in range(nv)]
+    want = [int(ai[s0:s0 + size] @ bi[s0:s0 + size]) for s0 in st]
+    assert np.array_equal(got, np.array(want, np.float32))
+    A = r.standard_normal((7, 64)).astype(np.float16)
+    x = r.standard_normal(64).astype(np.float16)
+    got = O.dot_product_fp16_fp32(A.view(np.uint16), np.tile(x, 7).view(np.uint16), 64, 7, 64)
+    assert np.array_equal(got, O.gemv_f16_f32(A.view(np.uint16), x.view(np.uint16)))
+
+
 def test_gemv_transpose_and_fp16():
     r = rng(4)
     A = r.integers(-4, 5, size=(300, 41)).astype(np.float32)

@@ -116,6 +116,11 @@ class GemvParams(Structure):
                 ("lda", c_uint32), ("trans", c_uint32), ("_pad0", c_uint32), ("_pad1", c_uint32)]
 
 
+class DotParams(Structure):
+    _fields_ = [("size", c_uint32), ("num_vectors", c_uint32), ("vector_stride", c_uint32),
+                ("_pad", c_uint32)]
+
+
 class GemvBatchedParams(Structure):
     _fields_ = [("M", c_uint32), ("N", c_uint32), ("alpha", c_float), ("beta", c_float),
                 ("lda", c_uint32), ("batch_count", c_uint32), ("stride_a", c_uint32),
@@ -154,6 +159,7 @@ EXPORTS = {
     "lux_hip_gemv_f32": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, POINTER(GemvParams)]),
     "lux_hip_gemv_f32_batched": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p,
                                          POINTER(GemvBatchedParams)]),
+    "lux_hip_dot_f16": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, POINTER(DotParams)]),
     "lux_hip_gemv_f16": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_uint32, c_uint32,
                                  c_uint32]),
     "lux_hip_buffer_wrap": (c_void_p, [c_void_p, c_void_p, c_size_t]),
@@ -367,6 +373,13 @@ class Context:
                               stride_x, stride_y, 0, 0, 0)
         self.plugin.check(self.lib.lux_hip_gemv_f32_batched(self.handle, a.handle, x.handle, y.handle,
                                                             byref(p)), "gemv_f32_batched")
+
+    def dot_f16(self, a: Buffer, b: Buffer, result: Buffer, size: int, num_vectors: int,
+                vector_stride: int):
+        """dot_product_fp16_fp32 (fp_quantized.wgsl:418-469); stride in elements."""
+        p = DotParams(size, num_vectors, vector_stride, 0)
+        self.plugin.check(self.lib.lux_hip_dot_f16(self.handle, a.handle, b.handle, result.handle,
+                                                   byref(p)), "dot_f16")
 
     def gemv_f16(self, a: Buffer, x: Buffer, y: Buffer, M: int, N: int, lda=None):
         self.plugin.check(self.lib.lux_hip_gemv_f16(self.handle, a.handle, x.handle, y.handle, M, N,

@@ -215,6 +215,8 @@ hipError_t launch_gemv_f32_t(const float* A, const float* x, float* y, int M, in
                              float alpha, float beta, hipStream_t s);
 hipError_t launch_gemm_f32(const float* A, const float* B, float* C, int M, int K, int N,
                            hipStream_t s);
+hipError_t launch_dot_f16(const void* a, const void* b, float* out, int size, int nv, size_t stride,
+                          hipStream_t s);
 hipError_t launch_gemv_f16(const void* A, const void* x, float* y, int M, int K, int lda,
                            hipStream_t s);
 // int4 weight-only GEMV, m == 1.

@@ -2,9 +2,10 @@
 //
 // Reference semantics: gemv.wgsl:49-96 (gemv_row_parallel: y = alpha*A.x + beta*y),
 // gemv.wgsl:103-149 (gemv_transpose), gemv.wgsl:297-354 (gemv_batched),
-// fp_quantized.wgsl:418-469 (fp16 products with fp32 accumulation) and WGSL_MATMUL (src/webgpu_plugin.cpp:138-205).  The sums are
-// reassociated (wave-wide partials instead of 256 strided lanes), which changes
-// rounding only.
+// fp_quantized.wgsl:418-469 (fp16 products with fp32 accumulation: the batched dot as
+// written, and a GEMV with a shared x) and WGSL_MATMUL (src/webgpu_plugin.cpp:138-205).
+// The sums are reassociated (wave-wide partials instead of 256 strided lanes), which
+// changes rounding only.
 #include <algorithm>
 
 #include "common.hpp"
@@ -227,16 +228,11 @@ __global__ __launch_bounds__(256) void k_gemm_f32(const float* __restrict__ A,
         }
 }
 
-// fp16 GEMV, fp32 accumulation: one wave per row, 16-byte chunks (8 halves),
-// v_dot2_f32_f16 on each pair (exact fp16 x fp16 products).
+// fp16 dot product of one row with fp32 accumulation, by one wave: 16-byte chunks (8
+// halves), v_dot2_f32_f16 on each pair (exact fp16 x fp16 products).  Wave-uniform result.
 template <bool VEC>
-__global__ __launch_bounds__(256) void k_gemv_f16(const f16* __restrict__ A,
-                                                  const f16* __restrict__ x,
-                                                  float* __restrict__ y, int M, int K, int lda) {
+__device__ __forceinline__ float f16_dot(const f16* __restrict__ a, const f16* __restrict__ x, int K) {
     const int lane = threadIdx.x & 63;
-    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (row >= M) return;
-    const f16* a = A + (size_t)row * lda;
     float acc0 = 0.f, acc1 = 0.f;
     if constexpr (VEC) {
         const f16x8* a8 = reinterpret_cast<const f16x8*>(a);
@@ -254,8 +250,31 @@ __global__ __launch_bounds__(256) void k_gemv_f16(const f16* __restrict__ A,
     } else {
         for (int k = lane; k < K; k += 64) acc0 = fmaf((float)a[k], (float)x[k], acc0);
     }
-    float s = wave_sum(acc0 + acc1);
-    if (lane == 0) y[row] = s;
+    return wave_sum(acc0 + acc1);
+}
+
+// fp16 GEMV: one wave per row of A against the shared x.
+template <bool VEC>
+__global__ __launch_bounds__(256) void k_gemv_f16(const f16* __restrict__ A,
+                                                  const f16* __restrict__ x,
+                                                  float* __restrict__ y, int M, int K, int lda) {
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= M) return;
+    const float s = f16_dot<VEC>(A + (size_t)row * lda, x, K);
+    if ((threadIdx.x & 63) == 0) y[row] = s;
+}
+
+// dot_product_fp16_fp32 (fp_quantized.wgsl:418-469): vector v of a and of b starts at
+// element 2 * (v * stride / 2) (the WGSL reads whole f16 pairs from word base / 2, so an
+// odd base starts one element early) and has `size` elements.  One wave per vector.
+template <bool VEC>
+__global__ __launch_bounds__(256) void k_dot_f16(const f16* __restrict__ a, const f16* __restrict__ b,
+                                                 float* __restrict__ out, int size, int nv, size_t stride) {
+    const int v = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (v >= nv) return;
+    const size_t e0 = 2 * ((size_t)v * stride / 2);
+    const float s = f16_dot<VEC>(a + e0, b + e0, size);
+    if ((threadIdx.x & 63) == 0) out[v] = s;
 }
 
 static inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
@@ -313,6 +332,17 @@ hipError_t launch_gemm_f32(const float* A, const float* B, float* C, int M, int 
                            hipStream_t s) {
     hipLaunchKernelGGL(k_gemm_f32, dim3((N + 63) / 64, (M + 63) / 64), dim3(256), 0, s, A, B, C,
                        M, K, N);
+    return hipGetLastError();
+}
+
+hipError_t launch_dot_f16(const void* a, const void* b, float* out, int size, int nv, size_t stride,
+                          hipStream_t s) {
+    const bool vec = stride % 8 == 0 && aligned16(a) && aligned16(b);
+    const f16* pa = reinterpret_cast<const f16*>(a);
+    const f16* pb = reinterpret_cast<const f16*>(b);
+    const dim3 grid((unsigned)(((int64_t)nv + 3) / 4)), block(256);
+    if (vec) hipLaunchKernelGGL(k_dot_f16<true>, grid, block, 0, s, pa, pb, out, size, nv, stride);
+    else hipLaunchKernelGGL(k_dot_f16<false>, grid, block, 0, s, pa, pb, out, size, nv, stride);
     return hipGetLastError();
 }
 

@@ -496,6 +496,25 @@ LUX_EXPORT LuxBackendError lux_hip_gemv_f32_batched(LuxBackendContext* ctx, LuxB
     return end_op(c, he, "gemv_f32_batched");
 }
 
+LUX_EXPORT LuxBackendError lux_hip_dot_f16(LuxBackendContext* ctx, LuxBackendBuffer* a, LuxBackendBuffer* b,
+                                           LuxBackendBuffer* result, const LuxHipDotParams* p) {
+    HipCtx* c = C(ctx);
+    HipBuf *A = B(a), *Bv = B(b), *R = B(result);
+    if (!c || !A || !Bv || !R || !p) return fail(LUX_BACKEND_ERROR_INVALID_ARGUMENT, "dot_f16: NULL argument");
+    const size_t size = p->size, nv = p->num_vectors, stride = p->vector_stride;
+    if (size > INT32_MAX || nv > INT32_MAX)
+        return fail(LUX_BACKEND_ERROR_INVALID_ARGUMENT, "dot_f16: size too large");
+    if (nv > 0) {
+        const size_t need = (2 * ((nv - 1) * stride / 2) + size) * 2;  // bytes of a and b
+        if (!fits(A, need) || !fits(Bv, need) || !fits(R, nv * 4))
+            return fail(LUX_BACKEND_ERROR_INVALID_ARGUMENT, "dot_f16: buffer too small");
+    }
+    if (LuxBackendError e = begin_op(c, "dot_f16")) return e;
+    if (nv == 0) return LUX_BACKEND_OK;
+    return end_op(c, launch_dot_f16(A->ptr, Bv->ptr, (float*)R->ptr, (int)size, (int)nv, stride, c->stream),
+                  "dot_f16");
+}
+
 LUX_EXPORT LuxBackendError lux_hip_gemv_f16(LuxBackendContext* ctx, LuxBackendBuffer* a,
                                             LuxBackendBuffer* x, LuxBackendBuffer* y, uint32_t M,
                                             uint32_t N, uint32_t lda) {

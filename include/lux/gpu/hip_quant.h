@@ -230,8 +230,9 @@ typedef struct LuxHipGemvParams {
 } LuxHipGemvParams;
 
 /* fp32 GEMV, replaces gemv_row_parallel / gemv_vec4 / gemv_tiled / gemv_simple
- * (trans 0, gemv.wgsl:49-96,155-274,360-381) and gemv_transpose (trans 1,
- * gemv.wgsl:103-149); bindings 0..3 of the WGSL become a, x, y, params. */
+ * (trans 0, gemv.wgsl:49-96,155-274,360-381), steel_gemv (trans 0, lda = N,
+ * steel/gemm/gemm.wgsl:186-220) and gemv_transpose (trans 1, gemv.wgsl:103-149);
+ * bindings 0..3 of the WGSL become a, x, y, params. */
 LuxBackendError lux_hip_gemv_f32(LuxBackendContext* ctx, LuxBackendBuffer* a,
                                  LuxBackendBuffer* x, LuxBackendBuffer* y,
                                  const LuxHipGemvParams* params);

@@ -204,3 +204,36 @@ def test_dot_f16(ctx, size, nv, stride):
         compare(got, ref, f"dot_f16 {size}x{nv}/{stride}", rel_tol=1e-5)
     with pytest.raises(W.LuxError):  # b one element short
         ctx.dot_f16(ab, ctx.upload(b[:n - 1]) if n > 1 else ctx.alloc(0), rb, size + 1, nv, stride)
+
+
+@pytest.mark.parametrize("M,N,lda", [(4096, 4096, 4096),   # the config-1 matrix, 16-B loads
+                                     (1000, 301, 301),     # scalar path, ragged strip
+                                     (20000, 64, 68),      # 256 row chunks of 79 rows
+                                     (37, 1024, 1024)])    # one partly filled chunk
+def test_gemv_f32_transpose_two_pass(ctx, M, N, lda):
+    """gemv_transpose (gemv.wgsl:103-149) through the two-pass kernel vs the oracle."""
+    r = rng(M + N)
+    A = r.standard_normal((M, lda)).astype(np.float32)
+    x = r.standard_normal(M).astype(np.float32)
+    y0 = r.standard_normal(N).astype(np.float32)
+    ref = oracle.gemv_transpose(np.ascontiguousarray(A[:, :N]), x, y0, 1.5, 0.5)
+    a, xb, yb = ctx.upload(A), ctx.upload(x), ctx.upload(y0)
+    ctx.gemv_f32(a, xb, yb, M, N, 1.5, 0.5, lda=lda, trans=True)
+    compare(ctx.download(yb, np.float32, N), ref, f"gemv_t {M}x{N}", rel_tol=1e-5)
+
+
+def test_gemv_f32_transpose_inf_and_empty(ctx):
+    """An inf in A gives inf in its column (no 0 * inf from the padding of a partly filled
+    chunk); M = 0 leaves y = beta * y."""
+    M, N = 37, 256
+    A = np.ones((M, N), np.float32)
+    A[0, 5] = np.inf
+    x = np.ones(M, np.float32)
+    a, xb, yb = ctx.upload(A), ctx.upload(x), ctx.alloc(N * 4)
+    ctx.gemv_f32(a, xb, yb, M, N, trans=True)
+    got = ctx.download(yb, np.float32, N)
+    assert got[5] == np.inf and np.all(got[np.arange(N) != 5] == M)
+    y0 = np.full(N, 2.0, np.float32)
+    yb2 = ctx.upload(y0)
+    ctx.gemv_f32(a, xb, yb2, 0, N, 1.0, 3.0, trans=True)
+    assert np.all(ctx.download(yb2, np.float32, N) == 6.0)

@@ -212,7 +212,8 @@ hipError_t launch_gemv_f32_batched(const float* A, const float* x, float* y, int
                                    float alpha, float beta, int batch, size_t sa, size_t sx,
                                    size_t sy, hipStream_t s);
 hipError_t launch_gemv_f32_t(const float* A, const float* x, float* y, int M, int N, int lda,
-                             float alpha, float beta, hipStream_t s);
+                             float alpha, float beta, float* workspace, hipStream_t s);
+size_t gemv_t_workspace(int M, int N);  // bytes of the transposed GEMV's partial sums
 hipError_t launch_gemm_f32(const float* A, const float* B, float* C, int M, int K, int N,
                            hipStream_t s);
 hipError_t launch_dot_f16(const void* a, const void* b, float* out, int size, int nv, size_t stride,

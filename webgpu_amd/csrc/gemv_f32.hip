@@ -161,30 +161,99 @@ __global__ __launch_bounds__(256) void k_gemv_f32_short(const float* __restrict_
     }
 }
 
-// y[n] = alpha * sum_r A[r, n] x[r] + beta*y[n]: lanes own columns (coalesced),
-// the 4 waves of a block split the rows, partials meet in LDS.
-__global__ __launch_bounds__(256) void k_gemv_f32_t(const float* __restrict__ A,
-                                                    const float* __restrict__ x,
-                                                    float* __restrict__ y, int M, int N,
-                                                    int lda, float alpha, float beta) {
-    __shared__ float part[4][64];
+// y[n] = alpha * sum_r A[r, n] x[r] + beta * y[n] (gemv_transpose) in two passes.  Pass 1:
+// a block takes a strip of 64 * CPL columns (CPL = 4 with 16-B loads) and a chunk of
+// rows; its 4 waves take every 4th row of the chunk, 8 rows in flight per lane, and their
+// sums meet in LDS: one partial per (chunk, column) in P[chunk][n].  Pass 2 adds the
+// chunks' partials in chunk order and applies alpha and beta.  Every sum has a fixed
+// order, so results are deterministic.  (One block per 64-column strip walking all rows,
+// one load in flight per lane, ran at 2 % of HBM on 4096 x 4096.)
+template <bool VEC>
+__global__ __launch_bounds__(256) void k_gemv_t_partial(const float* __restrict__ A, const float* __restrict__ x,
+                                                        float* __restrict__ P, int M, int N, int lda, int R) {
+    constexpr int CPL = VEC ? 4 : 1, U = 8;
+    __shared__ float red[4][64 * CPL];
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-    const int col = blockIdx.x * 64 + lane;
-    float acc = 0.f;
+    const int col = (blockIdx.x * 64 + lane) * CPL;
+    const int r0 = blockIdx.y * R, r1 = min(M, r0 + R);
+    float acc[CPL] = {};
     if (col < N) {
-        const int per = (M + 3) / 4;
-        const int r0 = wv * per, r1 = min(M, r0 + per);
-        for (int r = r0; r < r1; ++r) acc = fmaf(A[(size_t)r * lda + col], x[r], acc);
+        for (int r = r0 + wv; r < r1; r += 4 * U) {
+            float v[U][CPL], xv[U];
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int rr = r + 4 * u;
+                const bool in = rr < r1;
+                xv[u] = in ? x[rr] : 0.f;
+                // rows past the chunk reload row r and count as 0 (not 0 * A: A may hold inf)
+                const float* a = A + (size_t)(in ? rr : r) * lda + col;
+                if constexpr (VEC) {
+                    const f32x4 t = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(a));
+#pragma unroll
+                    for (int c = 0; c < CPL; ++c) v[u][c] = in ? t[c] : 0.f;
+                } else {
+                    const float t = __builtin_nontemporal_load(a);
+                    v[u][0] = in ? t : 0.f;
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < U; ++u)
+#pragma unroll
+                for (int c = 0; c < CPL; ++c) acc[c] = fmaf(v[u][c], xv[u], acc[c]);
+        }
     }
-    part[wv][lane] = acc;
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) red[wv][lane * CPL + c] = acc[c];
     __syncthreads();
     if (wv == 0 && col < N) {
-        float s = (part[0][lane] + part[1][lane]) + (part[2][lane] + part[3][lane]);
-        float r = alpha * s;
-        if (beta != 0.f) r = fmaf(beta, y[col], r);
-        y[col] = r;
+#pragma unroll
+        for (int c = 0; c < CPL; ++c) {
+            const int e = lane * CPL + c;
+            P[(size_t)blockIdx.y * N + col + c] = (red[0][e] + red[1][e]) + (red[2][e] + red[3][e]);
+        }
     }
 }
+
+// Pass 2: a block takes 64 columns; wave w adds chunks w, w + 4, ... (loads issued 8 at a
+// time), and the four sums meet in LDS in wave order.  (One thread per column walking all
+// chunks took 19 us for 64 chunks x 4096 columns: one load round trip per chunk.)
+__global__ __launch_bounds__(256) void k_gemv_t_reduce(const float* __restrict__ P, float* __restrict__ y, int N,
+                                                       int C, float alpha, float beta) {
+    __shared__ float red[4][64];
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int n = blockIdx.x * 64 + lane;
+    float s = 0.f;
+    if (n < N) {
+        for (int c0 = wv; c0 < C; c0 += 32) {
+            float v[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const int c = c0 + 4 * u;
+                v[u] = c < C ? P[(size_t)c * N + n] : 0.f;
+            }
+#pragma unroll
+            for (int u = 0; u < 8; ++u) s += v[u];
+        }
+    }
+    red[wv][lane] = s;
+    __syncthreads();
+    if (wv == 0 && n < N) {
+        float r = alpha * ((red[0][lane] + red[1][lane]) + (red[2][lane] + red[3][lane]));
+        if (beta != 0.f) r = fmaf(beta, y[n], r);  // y untouched when beta == 0
+        y[n] = r;
+    }
+}
+
+// Row chunks of the transposed GEMV: about 64 rows each, at most 256 chunks and at most
+// 16 Mi partials (64 MiB of workspace).
+static int gemv_t_chunks(int M, int N) {
+    int64_t c = ((int64_t)M + 63) / 64;
+    c = std::min<int64_t>(c, 256);
+    c = std::min<int64_t>(c, std::max<int64_t>(1, (int64_t)(16 << 20) / std::max(N, 1)));
+    return (int)std::max<int64_t>(c, 1);
+}
+
+size_t gemv_t_workspace(int M, int N) { return (size_t)gemv_t_chunks(M, N) * (size_t)N * sizeof(float); }
 
 // General fp32 GEMM C[M x N] = A[M x K] B[K x N] (row-major): 64x64 tile per
 // 256-thread block, 4x4 outputs per thread, K staged 16 at a time through LDS.
@@ -322,9 +391,16 @@ hipError_t launch_gemv_f32(const float* A, const float* x, float* y, int M, int 
 }
 
 hipError_t launch_gemv_f32_t(const float* A, const float* x, float* y, int M, int N, int lda,
-                             float alpha, float beta, hipStream_t s) {
-    hipLaunchKernelGGL(k_gemv_f32_t, dim3((N + 63) / 64), dim3(256), 0, s, A, x, y, M, N, lda,
-                       alpha, beta);
+                             float alpha, float beta, float* ws, hipStream_t s) {
+    const int C = gemv_t_chunks(M, N), R = (int)(((int64_t)M + C - 1) / C);
+    const bool vec = N % 4 == 0 && lda % 4 == 0 && aligned16(A);
+    if (vec)
+        hipLaunchKernelGGL(k_gemv_t_partial<true>, dim3((unsigned)((N + 255) / 256), (unsigned)C), dim3(256), 0, s,
+                           A, x, ws, M, N, lda, R);
+    else
+        hipLaunchKernelGGL(k_gemv_t_partial<false>, dim3((unsigned)((N + 63) / 64), (unsigned)C), dim3(256), 0, s,
+                           A, x, ws, M, N, lda, R);
+    hipLaunchKernelGGL(k_gemv_t_reduce, dim3((unsigned)((N + 63) / 64)), dim3(256), 0, s, ws, y, N, C, alpha, beta);
     return hipGetLastError();
 }
 

@@ -306,7 +306,9 @@ LuxBackendError hip_op_matmul_f32(LuxBackendContext* ctx, LuxBackendBuffer* a, L
         he = launch_gemv_f32(pa, pb, po, M, K, K, 1.0f, 0.0f, c->stream);
     } else if (M == 1) {
         // Row vector: C[N] = B^T[N x K] . a[K].
-        he = launch_gemv_f32_t(pb, pa, po, K, N, N, 1.0f, 0.0f, c->stream);
+        float* ws = static_cast<float*>(ensure_workspace(c, gemv_t_workspace(K, N)));
+        if (!ws) return fail(LUX_BACKEND_ERROR_OUT_OF_MEMORY, "op_matmul_f32: workspace allocation failed");
+        he = launch_gemv_f32_t(pb, pa, po, K, N, N, 1.0f, 0.0f, ws, c->stream);
     } else {
         he = launch_gemm_f32(pa, pb, po, M, K, N, c->stream);
     }
@@ -459,12 +461,16 @@ LUX_EXPORT LuxBackendError lux_hip_gemv_f32(LuxBackendContext* ctx, LuxBackendBu
     const size_t outn = p->trans ? N : M;
     if (outn == 0) return LUX_BACKEND_OK;
     hipError_t he;
-    if (p->trans)
+    if (p->trans) {
+        float* ws = static_cast<float*>(ensure_workspace(c, gemv_t_workspace((int)M, (int)N)));
+        if (!ws) return fail(LUX_BACKEND_ERROR_OUT_OF_MEMORY, "gemv_f32: workspace allocation failed");
         he = launch_gemv_f32_t((const float*)A->ptr, (const float*)X->ptr, (float*)Y->ptr, (int)M, (int)N,
-                               (int)lda, p->alpha, p->beta, c->stream);
-    else
+                               (int)lda, p->alpha, p->beta, ws, c->stream);
+    }
+    else {
         he = launch_gemv_f32((const float*)A->ptr, (const float*)X->ptr, (float*)Y->ptr, (int)M, (int)N,
                              (int)lda, p->alpha, p->beta, c->stream);
+    }
     return end_op(c, he, "gemv_f32");
 }
 

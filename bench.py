@@ -343,6 +343,33 @@ def bench_gemv_t(torch, W, ctx, steps, warmup):
                          "traffic": measured_traffic("gemvt")}}
 
 
+GH_BYTES = 14336 * 4096 * 2 + 4096 * 2 + 14336 * 4  # A (f16) + x read, y (f32) written
+
+
+def bench_gemv_f16(torch, W, ctx, steps, warmup):
+    """fp16 GEMV with fp32 accumulation: y[14336] = A[14336 x 4096] x (config 2's shape, fp16
+    weights)."""
+    r = np.random.default_rng(44)
+    A = (r.standard_normal((14336, 4096)) * 0.02).astype(np.float16)
+    x = r.standard_normal(4096).astype(np.float16)
+    copies = max(2, -(-512 * 2**20 // A.nbytes))
+    abs_ = [ctx.upload(A) for _ in range(copies)]
+    xb, yb = ctx.upload(x), ctx.alloc(14336 * 4)
+
+    def launch(i):
+        ctx.gemv_f16(abs_[i % copies], xb, yb, 14336, 4096)
+
+    n = max(3, min(steps, 100))
+    per = timed_graph(torch, ctx, launch, n, max(1, warmup // 4)) / n
+    for b in abs_ + [xb, yb]:
+        b.free()
+    gbs = GH_BYTES / per / 1e9
+    return {"us_per_launch": round(per * 1e6, 2), "value": round(gbs, 2), "unit": "GB/s",
+            "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS,
+                         "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
+                         "traffic": measured_traffic("gemvh")}}
+
+
 def bench_c5_fp(torch, W, ctx, steps, warmup):
     """Config 5 from fp32 activations: per-token int8 quantization (QUANTIZE_X) + W4A8."""
     from util import int4_weights
@@ -393,7 +420,7 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=10.0)
     ap.add_argument("--only", choices=["c1", "c2", "c3", "c4", "c5", "copy", "quant", "dequant", "gemvb",
-                                       "gemvt"],
+                                       "gemvt", "gemvh"],
                     default=None,
                     help="run one config only (profiling); the JSON line needs both")
     args = ap.parse_args()
@@ -444,6 +471,10 @@ def main():
         dq = bench_dequantize(torch, W, ctx, args.steps, args.warmup)
         log(f"  dequantize {dq['us_per_launch']} us/launch, {dq['value']} GB/s")
         return
+    if args.only == "gemvh":
+        gh = bench_gemv_f16(torch, W, ctx, args.steps, args.warmup)
+        log(f"  gemv_f16 {gh['us_per_launch']} us/launch, {gh['value']} GB/s")
+        return
     if args.only == "gemvt":
         gt = bench_gemv_t(torch, W, ctx, args.steps, args.warmup)
         log(f"  gemv_transpose {gt['us_per_launch']} us/launch, {gt['value']} GB/s")
@@ -464,7 +495,7 @@ def main():
         log(f"  C4 {c4['per_launch_s']*1e6:.1f} us/launch, {c4['tflops']:.1f} TFLOP/s")
     except W.LuxError as e:
         log(f"  C4 skipped: {e}")
-    c1, c3s, c5, c5f, qz, dq, gb, gt = None, [], None, None, None, None, None, None
+    c1, c3s, c5, c5f, qz, dq, gb, gt, gh = None, [], None, None, None, None, None, None, None
     try:
         log("bench: config 1 fp32 GEMV through op_matmul_f32")
         c1 = bench_c1(torch, W, ctx, args.steps, args.warmup)
@@ -491,6 +522,9 @@ def main():
         log("bench: transposed fp32 GEMV, 4096 x 4096")
         gt = bench_gemv_t(torch, W, ctx, args.steps, args.warmup)
         log(f"  gemv_transpose {gt['us_per_launch']} us/launch, {gt['value']} GB/s")
+        log("bench: fp16 GEMV, 14336 x 4096")
+        gh = bench_gemv_f16(torch, W, ctx, args.steps, args.warmup)
+        log(f"  gemv_f16 {gh['us_per_launch']} us/launch, {gh['value']} GB/s")
     except W.LuxError as e:
         log(f"  C1/C3/C5 skipped: {e}")
     cpu = None
@@ -536,6 +570,7 @@ def main():
         "dequantize_int4_g32_c4_weights": dq,
         "gemv_f32_batched": gb,
         "gemv_f32_transpose": gt,
+        "gemv_f16": gh,
     }
     print(json.dumps(out), flush=True)
     ctx.close()

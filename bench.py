@@ -233,6 +233,32 @@ def bench_c5(torch, W, ctx, steps, warmup):
                          "traffic": measured_traffic("c5"), "mfma_busy": measured_mfma_busy("c5")}}
 
 
+def bench_w8a8(torch, W, ctx, steps, warmup):
+    """W8A8 at config 5's shape: int8 weights 11008 x 4096 with fp16 g128 scales x int8
+    activations 256 x 4096 (per-token scales), fp16 out (matmul_int8 with group scales)."""
+    from util import int8_weights, quantize_rows_int8
+    r = np.random.default_rng(8)
+    q, _ = int8_weights(r, C5["n_out"], C5["k"])
+    s = r.uniform(0.001, 0.01, size=(C5["n_out"], C5["k"] // C5["gs"])).astype(np.float16)
+    a8, asc = quantize_rows_int8(r.standard_normal((C5["m"], C5["k"])).astype(np.float32))
+    wb, sb, xb, asb = ctx.upload(q), ctx.upload(s), ctx.upload(a8), ctx.upload(asc)
+    yb = ctx.alloc(C5["m"] * C5["n_out"] * 2)
+    d = W.qdesc(C5["n_out"], C5["k"], C5["m"], 8, C5["gs"], 0, W.SCALE_F16, W.I8, W.F16)
+
+    def launch(i):
+        ctx.qmatmul(d, wb, sb, xb, asb, yb)
+
+    n = max(3, min(steps, 100))
+    per = timed_graph(torch, ctx, launch, n, max(1, warmup // 4)) / n
+    ops = 2 * C5["m"] * C5["n_out"] * C5["k"]
+    tops = ops / per / 1e12
+    nbytes = q.nbytes + s.nbytes + a8.nbytes + asc.nbytes + C5["m"] * C5["n_out"] * 2
+    return {"us_per_launch": round(per * 1e6, 2), "value": round(tops, 2), "unit": "TOP/s",
+            "hbm_gbs": round(nbytes / per / 1e9, 2),
+            "roofline": {"bound": "mfma", "achieved": round(tops, 2), "peak": INT8_MFMA_PEAK_TOPS,
+                         "unit": "TOP/s", "frac": round(tops / INT8_MFMA_PEAK_TOPS, 4), "traffic": None}}
+
+
 QW_BYTES = 14336 * 4096 * 4 + 14336 * 4096 // 2 + 14336 * (4096 // 32) * 2  # read f32, write int4 + f16 scales
 
 
@@ -420,7 +446,7 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=10.0)
     ap.add_argument("--only", choices=["c1", "c2", "c3", "c4", "c5", "copy", "quant", "dequant", "gemvb",
-                                       "gemvt", "gemvh"],
+                                       "gemvt", "gemvh", "w8a8"],
                     default=None,
                     help="run one config only (profiling); the JSON line needs both")
     args = ap.parse_args()
@@ -471,6 +497,10 @@ def main():
         dq = bench_dequantize(torch, W, ctx, args.steps, args.warmup)
         log(f"  dequantize {dq['us_per_launch']} us/launch, {dq['value']} GB/s")
         return
+    if args.only == "w8a8":
+        w8 = bench_w8a8(torch, W, ctx, args.steps, args.warmup)
+        log(f"  W8A8 {w8['us_per_launch']} us/launch, {w8['value']} TOP/s, {w8['hbm_gbs']} GB/s")
+        return
     if args.only == "gemvh":
         gh = bench_gemv_f16(torch, W, ctx, args.steps, args.warmup)
         log(f"  gemv_f16 {gh['us_per_launch']} us/launch, {gh['value']} GB/s")
@@ -495,7 +525,7 @@ def main():
         log(f"  C4 {c4['per_launch_s']*1e6:.1f} us/launch, {c4['tflops']:.1f} TFLOP/s")
     except W.LuxError as e:
         log(f"  C4 skipped: {e}")
-    c1, c3s, c5, c5f, qz, dq, gb, gt, gh = None, [], None, None, None, None, None, None, None
+    c1, c3s, c5, c5f, qz, dq, gb, gt, gh, w8 = None, [], None, None, None, None, None, None, None, None
     try:
         log("bench: config 1 fp32 GEMV through op_matmul_f32")
         c1 = bench_c1(torch, W, ctx, args.steps, args.warmup)
@@ -510,6 +540,9 @@ def main():
         log("bench: config 5 from fp32 activations (per-token quantization + W4A8)")
         c5f = bench_c5_fp(torch, W, ctx, args.steps, args.warmup)
         log(f"  C5 fp32-x {c5f['us_per_launch']} us/launch, {c5f['value']} TOP/s")
+        log("bench: W8A8 at config 5's shape (int8 weights)")
+        w8 = bench_w8a8(torch, W, ctx, args.steps, args.warmup)
+        log(f"  W8A8 {w8['us_per_launch']} us/launch, {w8['value']} TOP/s")
         log("bench: int4 g32 quantizer on config-4 weights (fp32 -> int4 + fp16 scales)")
         qz = bench_quantize(torch, W, ctx, args.steps, args.warmup)
         log(f"  quantize {qz['us_per_launch']} us/launch, {qz['value']} GB/s")
@@ -566,6 +599,7 @@ def main():
         "int8_gemm_c3": c3s or None,
         "w4a8_gemm_c5": c5,
         "w4a8_c5_from_fp32_activations": c5f,
+        "w8a8_config5_shape": w8,
         "quantize_int4_g32_c4_weights": qz,
         "dequantize_int4_g32_c4_weights": dq,
         "gemv_f32_batched": gb,

@@ -448,11 +448,13 @@ def main():
     ap.add_argument("--only", choices=["c1", "c2", "c3", "c4", "c5", "copy", "quant", "dequant", "gemvb",
                                        "gemvt", "gemvh", "w8a8"],
                     default=None,
-                    help="run one config only (profiling); the JSON line needs both")
+                    help="run one leg only and log its timing (profiling); the JSON line comes "
+                         "from the full run")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (--gpus {args.gpus} requested); "
-              "the path shards over output channels with no communication, see DESIGN.md",
+              "the path would shard over weight rows (output channels), each GPU running "
+              "the same kernels on its rows with no communication",
               file=sys.stderr)
         sys.exit(2)
 

@@ -93,3 +93,73 @@ def test_graph_replays_match_eager(plugin):
             prev = got
     finally:
         c.close()
+
+
+def test_graph_codecs_and_gemv_forms(plugin):
+    """The dequantizer, the batched GEMV, the two-pass transposed GEMV (context workspace)
+    and the fp16 batched dot in one graph: three replays with new inputs, each equal bit
+    for bit to the same ops run eagerly."""
+    import torch
+    c = plugin.create_context(0)
+    try:
+        r = rng(4343)
+        rows, k, gs = 512, 1024, 32
+        _, Wq, sq = int4_weights(r, rows, k, gs)
+        B, Mb, Nb = 8, 256, 128
+        Ab = torch.tensor(r.standard_normal(B * Mb * Nb), dtype=torch.float32, device="cuda")
+        xb_t = torch.tensor(r.standard_normal(B * Nb), dtype=torch.float32, device="cuda")
+        Mt, Nt = 1000, 512
+        At = torch.tensor(r.standard_normal((Mt, Nt)), dtype=torch.float32, device="cuda")
+        xt_t = torch.tensor(r.standard_normal(Mt), dtype=torch.float32, device="cuda")
+        nv, size = 64, 1024
+        da = torch.tensor(r.standard_normal(nv * size), dtype=torch.float16, device="cuda")
+        db = torch.tensor(r.standard_normal(nv * size), dtype=torch.float16, device="cuda")
+
+        wq, s_q = c.upload(Wq), c.upload(sq)
+        ab, xbb, at, xtb, dab, dbb = c.wrap(Ab), c.wrap(xb_t), c.wrap(At), c.wrap(xt_t), c.wrap(da), c.wrap(db)
+        dq = W.quant_desc(rows, k, 4, gs, 0, W.SCALE_F16, W.F32)
+        shapes = {"deq": (rows * k * 4, np.float32, (rows, k)), "gb": (B * Mb * 4, np.float32, (B * Mb,)),
+                  "gt": (Nt * 4, np.float32, (Nt,)), "dot": (nv * 4, np.float32, (nv,))}
+
+        def outputs():
+            return {key: c.alloc(v[0]) for key, v in shapes.items()}
+
+        def run(o):
+            c.dequantize(dq, wq, s_q, o["deq"])
+            c.gemv_f32_batched(ab, xbb, o["gb"], Mb, Nb, B, Mb * Nb, Nb, Mb)
+            c.gemv_f32(at, xtb, o["gt"], Mt, Nt, trans=True)
+            c.dot_f16(dab, dbb, o["dot"], size, nv, size)
+
+        def fetch(o):
+            return {key: c.download(o[key], v[1], v[2]) for key, v in shapes.items()}
+
+        og, oe = outputs(), outputs()
+        run(og)  # sizes the workspace outside the capture
+        s = torch.cuda.Stream()
+        c.set_stream(s.cuda_stream)
+        c.set_synchronous(False)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            run(og)
+        c.set_stream(None)
+        c.set_synchronous(True)
+        prev = None
+        for i in range(3):
+            Ab.mul_(-0.5).add_(0.25 * (i + 1))
+            At.mul_(1.5).add_(-0.125)
+            da.mul_(0.75)
+            torch.cuda.synchronize()
+            with torch.cuda.stream(s):
+                g.replay()
+            torch.cuda.synchronize()
+            got = fetch(og)
+            run(oe)
+            ref = fetch(oe)
+            for key in shapes:
+                assert np.array_equal(got[key].view(np.uint8), ref[key].view(np.uint8)), f"replay {i}: {key}"
+            if prev is not None:
+                for key in ("gb", "gt", "dot"):
+                    assert not np.array_equal(got[key], prev[key]), f"replay {i}: {key} unchanged"
+            prev = got
+    finally:
+        c.close()

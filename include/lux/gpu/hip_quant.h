@@ -284,6 +284,25 @@ typedef struct LuxHipDotParams {
 LuxBackendError lux_hip_dot_f16(LuxBackendContext* ctx, LuxBackendBuffer* a, LuxBackendBuffer* b,
                                 LuxBackendBuffer* result, const LuxHipDotParams* params);
 
+/* ---- host packers: CPU code, no device or context -------------------------------
+ * The weight/scale codec on the host, for a loader that prepares quantized weights
+ * before upload; bit-identical to the device codecs above. */
+
+/* Pack n (a multiple of 8) int4 values in [-8, 7] into n / 8 words, element i of a word
+ * in bits 4i .. 4i+3: offset-binary q + 8 (pack_nax_int4_sym_x8, quantized_nax.wgsl:
+ * 94-102) or two's complement (the coding unpack_int4x8 reads, quantized.wgsl:148-156).
+ * A value outside [-8, 7] is refused with its index. */
+LuxBackendError lux_hip_pack_int4_host(const int8_t* q, size_t n, int coding, uint32_t* words);
+
+/* The inverse: n values from n / 8 words (unpack_nax_int4_sym_x8, quantized_nax.wgsl:
+ * 105-112, or unpack_int4x8, quantized.wgsl:148-156). */
+LuxBackendError lux_hip_unpack_int4_host(const uint32_t* words, size_t n, int coding, int8_t* q);
+
+/* lux_hip_convert_scales on host memory: F16 <-> F32 <-> GROUPSCALE (quantized_nax.wgsl:
+ * 49-54), binary16 by round to nearest even, a GROUPSCALE from F16/F32 as {s, 0, 0, 0}. */
+LuxBackendError lux_hip_convert_scales_host(const void* in, int in_format, void* out, int out_format,
+                                            size_t count);
+
 /* ---- buffer / stream plumbing (no reference counterpart: the WebGPU plugin
  * hides device addresses, src/webgpu_plugin.cpp:1564) ------------------------ */
 

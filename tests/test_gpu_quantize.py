@@ -310,3 +310,21 @@ def test_dequantize_roundtrip_and_rejects(ctx):
         ctx.dequantize(d, qb, sb, ctx.alloc(16))
     with pytest.raises(W.LuxError):  # an integer output type
         ctx.dequantize(W.quant_desc(rows, k, 4, gs, 0, W.SCALE_F32, W.I8), qb, sb, ob)
+
+
+def test_device_and_host_codecs_agree(ctx):
+    """lux_hip_convert_scales / convert_nibbles on the device and the host packers give the
+    same bits: binary16 rounding of subnormals, ties and overflow included."""
+    r = rng(99)
+    f = np.concatenate([r.standard_normal(4096), r.standard_normal(4096) * 1e-6,
+                        (np.arange(2048) + 0.5) * 2.0 ** -24, r.uniform(6e4, 7e4, 512),
+                        [0.0, -0.0, 65504.0, 65520.0, 2.0 ** -25]]).astype(np.float32)
+    n = f.size
+    b32, b16 = ctx.upload(f), ctx.alloc(n * 2)
+    ctx.convert_scales(b32, W.SCALE_F32, b16, W.SCALE_F16, n)
+    assert np.array_equal(ctx.download(b16, np.uint16, n), W.convert_scales_host(f, W.SCALE_F32, W.SCALE_F16))
+    q = r.integers(-8, 8, size=4096).astype(np.int8)
+    words = W.pack_int4_host(q, W.NIBBLE_OFFSET_BINARY)
+    wb, tb = ctx.upload(words), ctx.alloc(words.nbytes)
+    ctx.convert_nibbles(wb, tb, words.size, W.NIBBLE_OFFSET_BINARY, W.NIBBLE_TWOS_COMPLEMENT)
+    assert np.array_equal(ctx.download(tb, np.uint32, words.size), W.pack_int4_host(q, W.NIBBLE_TWOS_COMPLEMENT))

@@ -160,6 +160,9 @@ EXPORTS = {
     "lux_hip_gemv_f32_batched": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p,
                                          POINTER(GemvBatchedParams)]),
     "lux_hip_dot_f16": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, POINTER(DotParams)]),
+    "lux_hip_pack_int4_host": (c_int, [c_void_p, c_size_t, c_int, c_void_p]),
+    "lux_hip_unpack_int4_host": (c_int, [c_void_p, c_size_t, c_int, c_void_p]),
+    "lux_hip_convert_scales_host": (c_int, [c_void_p, c_int, c_void_p, c_int, c_size_t]),
     "lux_hip_gemv_f16": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_uint32, c_uint32,
                                  c_uint32]),
     "lux_hip_buffer_wrap": (c_void_p, [c_void_p, c_void_p, c_size_t]),
@@ -434,6 +437,49 @@ class Context:
         self.plugin.check(self.lib.lux_hip_requantize_i32(self.handle, src.handle, dst.handle,
                                                           size, input_scale, output_scale,
                                                           output_zero_point), "requantize")
+
+
+# --------------------------------------------------------------------------- host packers
+def _host_check(L, code: int, where: str):
+    if code != LUX_BACKEND_OK:
+        raise LuxError(code, where, (L.lux_hip_last_error() or b"").decode())
+
+
+def pack_int4_host(q, coding: int = 0) -> np.ndarray:
+    """lux_hip_pack_int4_host: int4 values (any shape, size % 8 == 0) -> uint32 words."""
+    L = load_library()
+    qa = np.ascontiguousarray(q, dtype=np.int8).reshape(-1)
+    out = np.empty(qa.size // 8, np.uint32)
+    _host_check(L, L.lux_hip_pack_int4_host(qa.ctypes.data, qa.size, coding, out.ctypes.data), "pack_int4_host")
+    return out
+
+
+def unpack_int4_host(words, n: int, coding: int = 0) -> np.ndarray:
+    """lux_hip_unpack_int4_host: n int4 values (int8) from n / 8 words."""
+    L = load_library()
+    wa = np.ascontiguousarray(words, dtype=np.uint32).reshape(-1)
+    if wa.size * 8 < n:
+        raise ValueError("unpack_int4_host: too few words")
+    out = np.empty(n, np.int8)
+    _host_check(L, L.lux_hip_unpack_int4_host(wa.ctypes.data, n, coding, out.ctypes.data), "unpack_int4_host")
+    return out
+
+
+_SCALE_NP = {SCALE_F16: (np.uint16, 1), SCALE_F32: (np.float32, 1), SCALE_GROUPSCALE: (np.uint32, 4)}
+
+
+def convert_scales_host(scales, in_format: int, out_format: int) -> np.ndarray:
+    """lux_hip_convert_scales_host.  F16 as uint16 bits, F32 as float32, GROUPSCALE as
+    uint32 [count, 4] records (scale and min/max are float bit patterns)."""
+    L = load_library()
+    idt, iw = _SCALE_NP[in_format]
+    odt, ow = _SCALE_NP[out_format]
+    a = np.ascontiguousarray(scales, dtype=idt).reshape(-1)
+    count = a.size // iw
+    out = np.empty(count * ow, odt)
+    _host_check(L, L.lux_hip_convert_scales_host(a.ctypes.data, in_format, out.ctypes.data, out_format, count),
+                "convert_scales_host")
+    return out.reshape(count, 4) if ow == 4 else out
 
 
 def quant_desc(rows: int, k: int, weight_bits: int = 4, group_size: int = 32,

@@ -16,6 +16,7 @@
 #include <algorithm>
 #include <chrono>
 #include <cstdarg>
+#include <cmath>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
@@ -859,4 +860,109 @@ LUX_EXPORT LuxBackendError lux_hip_requantize_i32(LuxBackendContext* ctx, LuxBac
     return end_op(c, launch_requantize(static_cast<const int32_t*>(I->ptr), static_cast<int32_t*>(O->ptr), size,
                                        input_scale, output_scale, output_zero_point, c->stream),
                   "requantize");
+}
+
+// ---------------------------------------------------------------- host packers
+// CPU-side producers of the hot path's inputs, for a loader that prepares weights on the
+// host before upload (no device, no context).  Bit-identical to the device codecs
+// (lux_hip_convert_nibbles, lux_hip_convert_scales).
+namespace {
+
+// binary32 -> binary16, round to nearest even (subnormals kept, overflow to inf, NaN
+// stays NaN with its top payload bits), the rounding the device's conversion uses.
+uint16_t host_f32_to_f16(float f) {
+    uint32_t x;
+    std::memcpy(&x, &f, 4);
+    const uint32_t sign = (x >> 16) & 0x8000u, ax = x & 0x7FFFFFFFu;
+    if (ax > 0x7F800000u) return (uint16_t)(sign | 0x7E00u | ((ax >> 13) & 0x3FFu));
+    if (ax >= 0x477FF000u) return (uint16_t)(sign | 0x7C00u);  // >= 65520 rounds to inf
+    const uint32_t eb = ax >> 23;
+    if (eb >= 113) {  // normal binary16: exponent eb - 127 + 15 >= 1
+        uint32_t h = ((eb - 112) << 10) | ((ax & 0x7FFFFFu) >> 13);
+        const uint32_t rem = ax & 0x1FFFu;
+        if (rem > 0x1000u || (rem == 0x1000u && (h & 1u))) ++h;  // a carry moves up the exponent
+        return (uint16_t)(sign | h);
+    }
+    if (eb < 102) return (uint16_t)sign;  // below 2^-25 (and 2^-25 itself ties to 0)
+    const uint32_t m = (ax & 0x7FFFFFu) | 0x800000u, r = 126 - eb;  // value = m * 2^-(24 + r)
+    uint32_t h = m >> r;
+    const uint32_t rem = m & ((1u << r) - 1u), half = 1u << (r - 1);
+    if (rem > half || (rem == half && (h & 1u))) ++h;  // may reach 0x400, the least normal
+    return (uint16_t)(sign | h);
+}
+
+float host_f16_to_f32(uint16_t h) {
+    const uint32_t sign = (uint32_t)(h & 0x8000u) << 16, e = (h >> 10) & 0x1Fu, m = h & 0x3FFu;
+    uint32_t x;
+    if (e == 0x1F) x = sign | 0x7F800000u | (m << 13);
+    else if (e) x = sign | ((e + 112) << 23) | (m << 13);
+    else if (!m) x = sign;
+    else {  // subnormal: m * 2^-24, exact in binary32
+        const float v = std::ldexp((float)m, -24);
+        std::memcpy(&x, &v, 4);
+        x |= sign;
+    }
+    float f;
+    std::memcpy(&f, &x, 4);
+    return f;
+}
+
+bool valid_coding(int c) { return c == LUX_HIP_NIBBLE_OFFSET_BINARY || c == LUX_HIP_NIBBLE_TWOS_COMPLEMENT; }
+
+}  // namespace
+
+LUX_EXPORT LuxBackendError lux_hip_pack_int4_host(const int8_t* q, size_t n, int coding, uint32_t* words) {
+    if (n % 8 != 0) return fail(LUX_BACKEND_ERROR_INVALID_ARGUMENT, "pack_int4_host: n = %zu is not a multiple of 8", n);
+    if (!valid_coding(coding)) return fail(LUX_BACKEND_ERROR_INVALID_ARGUMENT, "pack_int4_host: bad coding %d", coding);
+    if (n && (!q || !words)) return fail(LUX_BACKEND_ERROR_INVALID_ARGUMENT, "pack_int4_host: NULL argument");
+    const uint32_t ob = coding == LUX_HIP_NIBBLE_OFFSET_BINARY ? 8u : 0u;
+    for (size_t w = 0; w < n / 8; ++w) {
+        uint32_t word = 0;
+        for (int i = 0; i < 8; ++i) {
+            const int v = q[8 * w + i];
+            if (v < -8 || v > 7)
+                return fail(LUX_BACKEND_ERROR_INVALID_ARGUMENT, "pack_int4_host: value %d at %zu outside [-8, 7]", v,
+                            8 * w + i);
+            word |= (((uint32_t)v & 0xFu) ^ ob) << (4 * i);  // element i in bits 4i .. 4i+3
+        }
+        words[w] = word;
+    }
+    return LUX_BACKEND_OK;
+}
+
+LUX_EXPORT LuxBackendError lux_hip_unpack_int4_host(const uint32_t* words, size_t n, int coding, int8_t* q) {
+    if (n % 8 != 0) return fail(LUX_BACKEND_ERROR_INVALID_ARGUMENT, "unpack_int4_host: n = %zu is not a multiple of 8", n);
+    if (!valid_coding(coding)) return fail(LUX_BACKEND_ERROR_INVALID_ARGUMENT, "unpack_int4_host: bad coding %d", coding);
+    if (n && (!q || !words)) return fail(LUX_BACKEND_ERROR_INVALID_ARGUMENT, "unpack_int4_host: NULL argument");
+    const uint32_t ob = coding == LUX_HIP_NIBBLE_OFFSET_BINARY ? 8u : 0u;
+    for (size_t w = 0; w < n / 8; ++w)
+        for (int i = 0; i < 8; ++i) {
+            const uint32_t t = ((words[w] >> (4 * i)) & 0xFu) ^ ob;  // two's complement nibble
+            q[8 * w + i] = (int8_t)((int)t - (t >= 8 ? 16 : 0));
+        }
+    return LUX_BACKEND_OK;
+}
+
+LUX_EXPORT LuxBackendError lux_hip_convert_scales_host(const void* in, int in_format, void* out, int out_format,
+                                                       size_t count) {
+    if (scale_bytes(in_format) == 0 || scale_bytes(out_format) == 0)
+        return fail(LUX_BACKEND_ERROR_INVALID_ARGUMENT, "convert_scales_host: bad format");
+    if (count && (!in || !out)) return fail(LUX_BACKEND_ERROR_INVALID_ARGUMENT, "convert_scales_host: NULL argument");
+    for (size_t i = 0; i < count; ++i) {
+        float sc;
+        GroupScale g{};
+        if (in_format == LUX_HIP_SCALE_F16) sc = host_f16_to_f32(static_cast<const uint16_t*>(in)[i]);
+        else if (in_format == LUX_HIP_SCALE_F32) sc = static_cast<const float*>(in)[i];
+        else {
+            std::memcpy(&g, static_cast<const uint8_t*>(in) + 16 * i, 16);
+            sc = g.scale;
+        }
+        if (out_format == LUX_HIP_SCALE_F16) static_cast<uint16_t*>(out)[i] = host_f32_to_f16(sc);
+        else if (out_format == LUX_HIP_SCALE_F32) static_cast<float*>(out)[i] = sc;
+        else {
+            const GroupScale o = in_format == LUX_HIP_SCALE_GROUPSCALE ? g : GroupScale{sc, 0, 0.0f, 0.0f};
+            std::memcpy(static_cast<uint8_t*>(out) + 16 * i, &o, 16);
+        }
+    }
+    return LUX_BACKEND_OK;
 }

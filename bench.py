@@ -396,6 +396,54 @@ def bench_gemv_f16(torch, W, ctx, steps, warmup):
                          "traffic": measured_traffic("gemvh")}}
 
 
+FFN = dict(hidden=4096, inter=14336, gs=32)
+
+
+def ffn_bytes():
+    h, i, gs = FFN["hidden"], FFN["inter"], FFN["gs"]
+    w = 2 * i * h // 2 + 2 * i * (h // gs) * 2 + h * i // 2 + h * (i // gs) * 2  # int4 + fp16 scales
+    act = h * 4 * 2 + h * 4 + h * 2 * 2 + i * 2 * 2 + h * 4  # x (twice), gamma, normed, h, x_next
+    return w + act
+
+
+def bench_ffn(torch, W, ctx, steps, warmup):
+    """One decode step of a gated FFN through the plugin: rms_norm (f32 -> f16), int4 g32
+    gate/up GEMV with the SILU_MUL epilogue (2 x 14336 x 4096), int4 g32 down GEMV
+    (4096 x 14336) with the residual added in its ADD_RESIDUAL epilogue: three launches.
+    Weights rotate over copies beyond the MALL."""
+    from util import int4_weights
+    h, i, gs = FFN["hidden"], FFN["inter"], FFN["gs"]
+    r = np.random.default_rng(45)
+    _, Wgu, sgu = int4_weights(r, 2 * i, h, gs)
+    _, Wd, sd = int4_weights(r, h, i, gs)
+    copies = 3
+    wgu = [ctx.upload(Wgu) for _ in range(copies)]
+    s_gu = [ctx.upload(sgu) for _ in range(copies)]
+    wd = [ctx.upload(Wd) for _ in range(copies)]
+    s_d = [ctx.upload(sd) for _ in range(copies)]
+    x = ctx.upload(r.standard_normal(h).astype(np.float32))
+    gamma = ctx.upload(r.uniform(0.8, 1.2, h).astype(np.float32))
+    nb, hb, xn = ctx.alloc(h * 2), ctx.alloc(i * 2), ctx.alloc(h * 4)
+    d_gu = W.qdesc(2 * i, h, 1, 4, gs, 0, W.SCALE_F16, W.F16, W.F16)
+    d_d = W.qdesc(h, i, 1, 4, gs, 0, W.SCALE_F16, W.F16, W.F32)
+
+    def launch(j):
+        k = j % copies
+        ctx.rms_norm(x, gamma, nb, 1, h, 1e-6, W.F32, W.F16)
+        ctx.qmatmul_ex(d_gu, wgu[k], s_gu[k], nb, None, W.EPI_SILU_MUL, None, None, hb)
+        ctx.qmatmul_ex(d_d, wd[k], s_d[k], hb, None, W.EPI_ADD_RESIDUAL, None, x, xn)
+
+    n = max(3, min(steps, 60))
+    per = timed_graph(torch, ctx, launch, n, max(1, warmup // 4)) / n
+    for b in wgu + s_gu + wd + s_d + [x, gamma, nb, hb, xn]:
+        b.free()
+    gbs = ffn_bytes() / per / 1e9
+    return {"us_per_step": round(per * 1e6, 2), "value": round(gbs, 2), "unit": "GB/s",
+            "workload": f"hidden {h}, intermediate {i}, int4 g{gs} fp16 scales, m = 1",
+            "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS,
+                         "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None}}
+
+
 def bench_c5_fp(torch, W, ctx, steps, warmup):
     """Config 5 from fp32 activations: per-token int8 quantization (QUANTIZE_X) + W4A8."""
     from util import int4_weights
@@ -446,7 +494,7 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=10.0)
     ap.add_argument("--only", choices=["c1", "c2", "c3", "c4", "c5", "copy", "quant", "dequant", "gemvb",
-                                       "gemvt", "gemvh", "w8a8"],
+                                       "gemvt", "gemvh", "w8a8", "ffn"],
                     default=None,
                     help="run one leg only and log its timing (profiling); the JSON line comes "
                          "from the full run")
@@ -499,6 +547,10 @@ def main():
         dq = bench_dequantize(torch, W, ctx, args.steps, args.warmup)
         log(f"  dequantize {dq['us_per_launch']} us/launch, {dq['value']} GB/s")
         return
+    if args.only == "ffn":
+        ff = bench_ffn(torch, W, ctx, args.steps, args.warmup)
+        log(f"  decode FFN step {ff['us_per_step']} us/step, {ff['value']} GB/s")
+        return
     if args.only == "w8a8":
         w8 = bench_w8a8(torch, W, ctx, args.steps, args.warmup)
         log(f"  W8A8 {w8['us_per_launch']} us/launch, {w8['value']} TOP/s, {w8['hbm_gbs']} GB/s")
@@ -527,7 +579,7 @@ def main():
         log(f"  C4 {c4['per_launch_s']*1e6:.1f} us/launch, {c4['tflops']:.1f} TFLOP/s")
     except W.LuxError as e:
         log(f"  C4 skipped: {e}")
-    c1, c3s, c5, c5f, qz, dq, gb, gt, gh, w8 = None, [], None, None, None, None, None, None, None, None
+    c1, c3s, c5, c5f, qz, dq, gb, gt, gh, w8, ff = None, [], None, None, None, None, None, None, None, None, None
     try:
         log("bench: config 1 fp32 GEMV through op_matmul_f32")
         c1 = bench_c1(torch, W, ctx, args.steps, args.warmup)
@@ -560,6 +612,9 @@ def main():
         log("bench: fp16 GEMV, 14336 x 4096")
         gh = bench_gemv_f16(torch, W, ctx, args.steps, args.warmup)
         log(f"  gemv_f16 {gh['us_per_launch']} us/launch, {gh['value']} GB/s")
+        log("bench: decode FFN step (rms_norm, gate/up + SILU_MUL, down + residual)")
+        ff = bench_ffn(torch, W, ctx, args.steps, args.warmup)
+        log(f"  decode FFN step {ff['us_per_step']} us/step, {ff['value']} GB/s")
     except W.LuxError as e:
         log(f"  C1/C3/C5 skipped: {e}")
     cpu = None
@@ -607,6 +662,7 @@ def main():
         "gemv_f32_batched": gb,
         "gemv_f32_transpose": gt,
         "gemv_f16": gh,
+        "decode_ffn_step": ff,
     }
     print(json.dumps(out), flush=True)
     ctx.close()

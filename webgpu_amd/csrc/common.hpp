@@ -221,6 +221,7 @@ hipError_t launch_dot_f16(const void* a, const void* b, float* out, int size, in
 hipError_t launch_gemv_f16(const void* A, const void* x, float* y, int M, int K, int lda,
                            hipStream_t s);
 // int4 weight-only GEMV, m == 1.
+bool qgemv_i4_fast(const QArgs& a);  // the m = 1 int4 GEMV fast path applies (SiluMul needs it)
 hipError_t launch_qgemv_i4(const QArgs& a, hipStream_t s);
 // Weight-only int4/int8 matmul for small m (bandwidth regime), fp16/bf16/f32 X.
 bool qgemm_small_supported(const QArgs& a);

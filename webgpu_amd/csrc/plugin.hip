@@ -651,7 +651,7 @@ LuxBackendError qmatmul_impl(LuxBackendContext* ctx, const LuxHipQMatmulDesc* d,
         if (!w4a8_supported(a))
             return fail(LUX_BACKEND_ERROR_NOT_SUPPORTED, "qmatmul: W4A8/W8A8 shape/format not supported");
         he = launch_w4a8(a, c->stream);
-    } else if (d->weight_bits == 4 && M == 1 && !silu_mul) {
+    } else if (d->weight_bits == 4 && M == 1 && (!silu_mul || qgemv_i4_fast(a))) {
         he = launch_qgemv_i4(a, c->stream);
     } else if (M <= 64 && qgemm_small_supported(a)) {
         // decode batches: bandwidth regime, weights streamed once per 64 tokens

@@ -51,7 +51,10 @@ __device__ __forceinline__ float dot_slice_sub(const uint32_t (&q)[4], const f16
 // row r+D and consumes row r, so the math of row r overlaps the loads of later rows.
 // x is read from HBM/L2 once per block (one 16-byte chunk per thread and SPL pass) and
 // shared through LDS.  The host sizes the grid to 8 waves per CU with equal rows per wave.
-template <int SPL, int RW, int D, ScaleKind SK, YKind YK, bool XOR>
+// SM (SiluMul epilogue): the wave's rows are read as interleaved pairs, gate row g then
+// up row n_out/2 + g (virtual row v -> v even: v/2, v odd: n_out/2 + v/2; RW is even, so a
+// pair never straddles two waves), and lane 2p stores silu(gate) * up to y[g].
+template <int SPL, int RW, int D, ScaleKind SK, YKind YK, bool XOR, bool SM>
 __global__ __launch_bounds__(256) void k_qgemv_i4_f16(const u32x4* __restrict__ W,
                                                       const void* __restrict__ S,
                                                       const f16* __restrict__ x,
@@ -86,7 +89,8 @@ __global__ __launch_bounds__(256) void k_qgemv_i4_f16(const u32x4* __restrict__ 
     // they are computed but never stored.  Straight-line, in-order issue keeps the
     // waitcnt bookkeeping exact.
     auto issue = [&](int r) {
-        const size_t row = (size_t)min(row0 + r, n_out - 1);
+        const int v = min(row0 + r, n_out - 1);
+        const size_t row = SM ? (size_t)((v & 1) ? (n_out >> 1) + (v >> 1) : (v >> 1)) : (size_t)v;
 #pragma unroll
         for (int j = 0; j < SPL; ++j) {
             q[r][j] = __builtin_nontemporal_load(W + row * s_row + sl[j]);
@@ -152,7 +156,12 @@ __global__ __launch_bounds__(256) void k_qgemv_i4_f16(const u32x4* __restrict__ 
         res = lane == r ? acc : res;
         __builtin_amdgcn_sched_barrier(0);
     }
-    if (lane < nrows) store_y<YK>(y, row0 + lane, apply_epi(res, epi, 0, row0 + lane, n_out));
+    if constexpr (SM) {
+        const float up = __shfl_down(res, 1, 64);  // the pair's up row sits in the next lane
+        if (lane < nrows && !(lane & 1)) store_y<YK>(y, (row0 + lane) >> 1, silu_f(res) * up);
+    } else {
+        if (lane < nrows) store_y<YK>(y, row0 + lane, apply_epi(res, epi, 0, row0 + lane, n_out));
+    }
 }
 
 // Any activation dtype, any group size that is a multiple of 8: one wave per row,
@@ -199,12 +208,20 @@ static void launch_rwd(const QArgs& a, hipStream_t s) {
     const dim3 grid((waves + 3) / 4), block(256);
     const u32x4* w = reinterpret_cast<const u32x4*>(a.w);
     const f16* x = reinterpret_cast<const f16*>(a.x);
-    if (a.xor_mask)
-        hipLaunchKernelGGL((k_qgemv_i4_f16<SPL, RW, D, SK, YK, true>), grid, block, 0, s, w, a.s, x,
-                           a.y, a.n_out, a.k, __builtin_ctz(a.group_size / 32), a.xor_mask, a.epi);
-    else
-        hipLaunchKernelGGL((k_qgemv_i4_f16<SPL, RW, D, SK, YK, false>), grid, block, 0, s, w, a.s, x,
-                           a.y, a.n_out, a.k, __builtin_ctz(a.group_size / 32), a.xor_mask, a.epi);
+    const int shift = __builtin_ctz(a.group_size / 32);
+    auto go = [&](auto kern) {
+        hipLaunchKernelGGL(kern, grid, block, 0, s, w, a.s, x, a.y, a.n_out, a.k, shift, a.xor_mask, a.epi);
+    };
+    const bool sm = a.epi.kind == (int)Epi::SiluMul;
+    if constexpr (RW % 2 == 0) {
+        if (sm) {
+            if (a.xor_mask) go(k_qgemv_i4_f16<SPL, RW, D, SK, YK, true, true>);
+            else go(k_qgemv_i4_f16<SPL, RW, D, SK, YK, false, true>);
+            return;
+        }
+    }
+    if (a.xor_mask) go(k_qgemv_i4_f16<SPL, RW, D, SK, YK, true, false>);
+    else go(k_qgemv_i4_f16<SPL, RW, D, SK, YK, false, false>);
 }
 
 // Two rows of prefetch (issue row r+2, then compute row r) measured best on MI355X for
@@ -224,6 +241,7 @@ static void launch_fast(const QArgs& a, hipStream_t s) {
     const int target_waves = device_cus() * 8;
     int rw = (a.n_out + target_waves - 1) / target_waves;
     rw = rw < 1 ? 1 : (rw > RWMAX ? RWMAX : rw);
+    if (a.epi.kind == (int)Epi::SiluMul) rw += rw & 1;  // whole gate/up pairs per wave (RWMAX is even)
     switch (rw) {
         case 1: launch_rw<SPL, 1, SK, YK>(a, s); break;
         case 2: launch_rw<SPL, 2, SK, YK>(a, s); break;
@@ -279,13 +297,18 @@ static bool launch_generic(const QArgs& a, hipStream_t s) {
     }
 }
 
-hipError_t launch_qgemv_i4(const QArgs& a, hipStream_t s) {
-    // slices per group must be a power of two (the kernel shifts instead of dividing)
+bool qgemv_i4_fast(const QArgs& a) {
+    // slices per group must be a power of two (the kernel shifts instead of dividing);
+    // up to 8 slices per lane (k <= 16384)
     const int spg = a.group_size / 32;
-    const bool fast = a.x_kind == XKind::F16 && a.k % 32 == 0 && a.group_size % 32 == 0 &&
-                      spg > 0 && (spg & (spg - 1)) == 0 &&
-                      (a.scale_kind != ScaleKind::F16 || (a.k / a.group_size) % 2 == 0) &&
-                      ((uintptr_t)a.w & 15u) == 0 && ((uintptr_t)a.x & 15u) == 0;
+    return a.x_kind == XKind::F16 && a.k % 32 == 0 && a.k <= 16384 && a.group_size % 32 == 0 && spg > 0 &&
+           (spg & (spg - 1)) == 0 && (a.scale_kind != ScaleKind::F16 || (a.k / a.group_size) % 2 == 0) &&
+           a.scale_kind != ScaleKind::None && ((uintptr_t)a.w & 15u) == 0 && ((uintptr_t)a.x & 15u) == 0;
+}
+
+hipError_t launch_qgemv_i4(const QArgs& a, hipStream_t s) {
+    const bool fast = qgemv_i4_fast(a);
+    if (a.epi.kind == (int)Epi::SiluMul && !fast) return hipErrorInvalidValue;  // the caller checks
     bool launched = false;
     if (fast) {
         switch (a.scale_kind) {

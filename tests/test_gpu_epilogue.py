@@ -64,7 +64,7 @@ ALL = [W.EPI_RELU, W.EPI_GELU, W.EPI_SILU, W.EPI_TANH, W.EPI_SIGMOID, W.EPI_ADD_
 
 @pytest.mark.parametrize("epi", ALL)
 def test_epilogue_int4_gemv(ctx, epi):
-    """m = 1: the GEMV kernel (SILU_MUL runs on the small-m kernel)."""
+    """m = 1: the GEMV kernel (SILU_MUL reads the gate and up rows as interleaved pairs)."""
     got, ref = _case(ctx, rng(100 + epi), 4, 1024, 4096, 1, 32, "f16", "f16", epi)
     compare(got, ref, f"GEMV epilogue {epi}")
 
@@ -116,3 +116,37 @@ def test_epilogue_large_m_config4_shape(ctx, epi, ydt):
     ~1e-3 rel-L2 against the rounded oracle."""
     got, ref = _case(ctx, rng(400 + epi), 4, 14336, 256, 2048, 32, "bf16", ydt, epi)
     compare(got, ref, f"config-4-shape epilogue {epi} {ydt}")
+
+
+@pytest.mark.parametrize("n_out,K,gs,coding,sfmt,xdt", [
+    (666, 512, 32, W.NIBBLE_TWOS_COMPLEMENT, W.SCALE_F32, "f16"),  # 333 pairs, xor-decoded nibbles
+    (2 * 14336, 4096, 32, W.NIBBLE_OFFSET_BINARY, W.SCALE_F16, "f16"),  # 8 rows (4 pairs) per wave
+    (512, 1024, 128, W.NIBBLE_OFFSET_BINARY, W.SCALE_GROUPSCALE, "f16"),
+    (512, 1024, 32, W.NIBBLE_OFFSET_BINARY, W.SCALE_F16, "bf16"),  # no fast GEMV: small-m kernel
+])
+def test_silu_mul_gemv_pairs(ctx, n_out, K, gs, coding, sfmt, xdt):
+    """SILU_MUL at m = 1 across codings, scale formats and pair counts, against
+    silu_mul of the fp64 matmul (steel_gemm_fused.wgsl:452-558)."""
+    r = rng(n_out + K + gs)
+    _, Wp, s16 = int4_weights(r, n_out, K, gs, coding)
+    sf = s16.astype(np.float32)
+    if sfmt == W.SCALE_F16:
+        sbuf = s16
+    elif sfmt == W.SCALE_F32:
+        sbuf = sf
+    else:
+        sbuf = np.zeros(sf.shape + (4,), np.float32)
+        sbuf[..., 0] = sf
+    xf = r.standard_normal((1, K)).astype(np.float32)
+    if xdt == "bf16":
+        xin = bf16_bits(xf)
+        xf = bf16_to_f32(xin)
+    else:
+        xin = xf.astype(np.float16)
+        xf = xin.astype(np.float32)
+    w_ob = Wp if coding == W.NIBBLE_OFFSET_BINARY else Wp ^ np.uint32(0x88888888)
+    ref = oracle.silu_mul(oracle.qmatmul_f64(w_ob, sf, xf, gs, 4).astype(np.float32))
+    d = W.qdesc(n_out, K, 1, 4, gs, coding, sfmt, W.BF16 if xdt == "bf16" else W.F16, W.F32)
+    yb = ctx.alloc(n_out // 2 * 4)
+    ctx.qmatmul_ex(d, ctx.upload(Wp), ctx.upload(sbuf), ctx.upload(xin), None, W.EPI_SILU_MUL, None, None, yb)
+    compare(ctx.download(yb, np.float32, (1, n_out // 2)).astype(np.float64), ref, f"SILU_MUL GEMV {n_out}x{K}")

@@ -213,10 +213,11 @@ __global__ __launch_bounds__(256) void k_quantize_large(const void* __restrict__
 
 // Groups of 513 .. 2048 * CPT elements (per-row scales of activations and weights): one
 // 256-thread block per group, CPT chunks of 8 per thread held in registers, one pass.
-template <XKind XK, int BITS, ScaleKind SK, int CPT>
-__global__ __launch_bounds__(256) void k_quantize_rows(const void* __restrict__ X, void* __restrict__ Q,
-                                                       void* __restrict__ S, int cpg, uint32_t ob) {
-    __shared__ float red[2][4];
+template <XKind XK, int BITS, ScaleKind SK, int CPT, int NT = 256>
+__global__ __launch_bounds__(NT) void k_quantize_rows(const void* __restrict__ X, void* __restrict__ Q,
+                                                      void* __restrict__ S, int cpg, uint32_t ob) {
+    constexpr int NW = NT / 64;
+    __shared__ float red[2][NW];
     const size_t g = blockIdx.x;
     const int tid = threadIdx.x;
     const size_t c0 = g * (size_t)cpg;
@@ -224,7 +225,7 @@ __global__ __launch_bounds__(256) void k_quantize_rows(const void* __restrict__ 
     float mx = -1e30f, mn = 1e30f;
 #pragma unroll
     for (int j = 0; j < CPT; ++j) {
-        const int cc = tid + 256 * j;
+        const int cc = tid + NT * j;
         if (cc < cpg) {
             load8<XK>(X, c0 + cc, v[j]);
 #pragma unroll
@@ -244,15 +245,20 @@ __global__ __launch_bounds__(256) void k_quantize_rows(const void* __restrict__ 
         red[1][tid >> 6] = mn;
     }
     __syncthreads();
-    mx = fmaxf(fmaxf(red[0][0], red[0][1]), fmaxf(red[0][2], red[0][3]));
-    mn = fminf(fminf(red[1][0], red[1][1]), fminf(red[1][2], red[1][3]));
+    mx = red[0][0];
+    mn = red[1][0];
+#pragma unroll
+    for (int w = 1; w < NW; ++w) {
+        mx = fmaxf(mx, red[0][w]);
+        mn = fminf(mn, red[1][w]);
+    }
     const float s = group_scale<BITS>(mx, mn);
     const float sq = stored_scale<SK>(s);
     if (tid == 0) store_scale<SK>(S, g, s, mn, mx);
     const QStep<BITS> qs(sq);
 #pragma unroll
     for (int j = 0; j < CPT; ++j) {
-        const int cc = tid + 256 * j;
+        const int cc = tid + NT * j;
         if (cc < cpg) {
             int q[8];
 #pragma unroll
@@ -382,7 +388,9 @@ static hipError_t launch_q3(const QuantArgs& a, hipStream_t s) {
         const size_t groups = (size_t)a.rows * (a.k / a.group_size);
         const int cpt = (lpg + 255) / 256;  // chunks per thread with a block per group
         const dim3 gb((unsigned)groups), block(256);
-        if (cpt <= 1) hipLaunchKernelGGL((k_quantize_rows<XK, BITS, SK, 1>), gb, block, 0, s, a.x, a.q, a.s, lpg, ob);
+        if (lpg > 256 && lpg <= 512)  // one chunk per thread, 8 waves per group
+            hipLaunchKernelGGL((k_quantize_rows<XK, BITS, SK, 1, 512>), gb, dim3(512), 0, s, a.x, a.q, a.s, lpg, ob);
+        else if (cpt <= 1) hipLaunchKernelGGL((k_quantize_rows<XK, BITS, SK, 1>), gb, block, 0, s, a.x, a.q, a.s, lpg, ob);
         else if (cpt <= 2) hipLaunchKernelGGL((k_quantize_rows<XK, BITS, SK, 2>), gb, block, 0, s, a.x, a.q, a.s, lpg, ob);
         else if (cpt <= 4) hipLaunchKernelGGL((k_quantize_rows<XK, BITS, SK, 4>), gb, block, 0, s, a.x, a.q, a.s, lpg, ob);
         else if (cpt <= 8) hipLaunchKernelGGL((k_quantize_rows<XK, BITS, SK, 8>), gb, block, 0, s, a.x, a.q, a.s, lpg, ob);

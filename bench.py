@@ -37,6 +37,7 @@ C3 = dict(n_out=28672, k=8192)
 C5 = dict(n_out=11008, k=4096, m=256, gs=128)
 INT8_MFMA_PEAK_TOPS = 5000.0
 COPY_BYTES = 512 * 2**20
+SPIN_CYCLES = 200_000  # device spin ahead of the timed replay (~0.1 ms of shader clocks)
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "hbm_traffic.md")
 MFMA_FILE = os.path.join(ROOT, "profiles", "mfma_utilization.md")
 
@@ -74,8 +75,14 @@ def log(msg):
 def timed_graph(torch, ctx, launch, steps: int, warmup: int, settle_s: float = 0.025):
     """Warm up eagerly (`warmup` launches), capture `steps` launches into one graph,
     replay it untimed until the GPU has run this workload for `settle_s` seconds (the
-    first replays after a switch of workload run at lower clocks), then time one
-    replay.  Returns seconds for the timed replay."""
+    first replays after a switch of workload run at lower clocks), then time exactly
+    one replay (`steps` launches) with HIP events on the launch stream.
+
+    The timed replay is queued behind a short device-side spin and one more untimed
+    replay, so every packet of it is already in the queue when the GPU reaches the
+    first event: the events bracket the K launches back to back, without the host's
+    graph-launch latency (tens of microseconds, which would otherwise be spread over
+    the K launches).  Returns seconds for the timed replay."""
     s = torch.cuda.Stream()
     ctx.set_stream(s.cuda_stream)
     ctx.set_synchronous(False)
@@ -96,10 +103,12 @@ def timed_graph(torch, ctx, launch, steps: int, warmup: int, settle_s: float = 0
     e0 = torch.cuda.Event(enable_timing=True)
     e1 = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
-    e0.record(s)
     with torch.cuda.stream(s):
+        torch.cuda._sleep(SPIN_CYCLES)  # holds the queue while the host enqueues the rest
+        g.replay()                      # untimed: keeps the clocks at the workload's level
+        e0.record(s)
         g.replay()
-    e1.record(s)
+        e1.record(s)
     e1.synchronize()
     torch.cuda.synchronize()
     ctx.set_stream(None)
@@ -468,6 +477,28 @@ def bench_c5_fp(torch, W, ctx, steps, warmup):
                          "traffic": None}}
 
 
+def host_cpu():
+    """CPU model string and the host's logical CPU count as this process sees them."""
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    try:
+        avail = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        avail = os.cpu_count()
+    return model, os.cpu_count(), avail
+
+
+CPU_LABEL = ("CPU restatement, not SwiftShader: oracle/lux_oracle.c (the reference WGSL's "
+             "arithmetic in C, OpenMP); Dawn/SwiftShader is not in this image")
+
+
 def cpu_baseline_c2(Wp, s, x, budget_s=10.0):
     import oracle
     sf = s.astype(np.float32).reshape(-1)
@@ -480,10 +511,42 @@ def cpu_baseline_c2(Wp, s, x, budget_s=10.0):
         el = time.perf_counter() - t0
         if el >= budget_s or n >= 200:
             break
+    model, ncpu, avail = host_cpu()
     return {"value": round(C2_BYTES * n / el / 1e9, 3), "unit": "GB/s",
-            "cores": oracle.num_threads(), "kind": "port",
+            "cores": oracle.num_threads(), "kind": "port", "label": CPU_LABEL,
+            "cpu_model": model, "nproc": avail, "host_logical_cpus": ncpu,
             "sample": f"full config-2 GEMV (14336x4096 int4 g32) x{n} calls in {el:.1f} s, "
-                      "oracle/lux_oracle.c lo_matmul_nax_grouped (WGSL restatement, OpenMP)"}
+                      "lo_matmul_nax_grouped (matmul_nax_grouped, quantized_nax.wgsl:568-626)"}
+
+
+C4_CPU_TOKENS = 32  # bounded CPU sample of config 4: 32 of the 2048 activation rows
+
+
+def cpu_baseline_c4(budget_s=10.0):
+    """Config 4 on the host: the oracle's matmul_nax_grouped over the full 14336 x 4096
+    int4 g32 weights and a 32-token slice of the activations (the work per token is the
+    same at any M, so TFLOP/s scales; 2048 tokens would take minutes)."""
+    import oracle
+    from util import int4_weights
+    r = np.random.default_rng(4)
+    _, Wp, s = int4_weights(r, C4["n_out"], C4["k"], C4["gs"])
+    sf = s.astype(np.float32).reshape(-1)
+    act = r.standard_normal((C4["k"], C4_CPU_TOKENS)).astype(np.float32)
+    oracle.matmul_nax_grouped(Wp, sf, act, C4["gs"])  # warm
+    n, t0 = 0, time.perf_counter()
+    while True:
+        oracle.matmul_nax_grouped(Wp, sf, act, C4["gs"])
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s or n >= 50:
+            break
+    flops = 2 * C4_CPU_TOKENS * C4["n_out"] * C4["k"] * n
+    model, ncpu, avail = host_cpu()
+    return {"value": round(flops / el / 1e12, 5), "unit": "TFLOP/s",
+            "cores": oracle.num_threads(), "kind": "port", "label": CPU_LABEL,
+            "cpu_model": model, "nproc": avail, "host_logical_cpus": ncpu,
+            "sample": f"config-4 weights (14336x4096 int4 g32) x {C4_CPU_TOKENS} of the 2048 tokens, "
+                      f"x{n} calls in {el:.1f} s; TFLOP/s of that sample"}
 
 
 def main():
@@ -617,11 +680,14 @@ def main():
         log(f"  decode FFN step {ff['us_per_step']} us/step, {ff['value']} GB/s")
     except W.LuxError as e:
         log(f"  C1/C3/C5 skipped: {e}")
-    cpu = None
+    cpu, cpu4 = None, None
     if not args.no_cpu_baseline:
         log("bench: CPU baseline (oracle)")
         cpu = cpu_baseline_c2(c2["W"], c2["s"], c2["x"], args.cpu_budget)
         log(f"  CPU {cpu['value']} GB/s on {cpu['cores']} threads")
+        log("bench: CPU baseline, config 4 sample (oracle)")
+        cpu4 = cpu_baseline_c4(args.cpu_budget)
+        log(f"  CPU C4 sample {cpu4['value']} TFLOP/s on {cpu4['cores']} threads")
 
     gbs = c2["gbs"]
     out = {
@@ -640,7 +706,8 @@ def main():
         "config": {"workload": "config 2: int4 g32 weight-only GEMV, W 14336x4096 offset-binary, "
                                "fp16 scales U(0.005,0.02), x fp16 N(0,1), y fp16",
                    "n_out": 14336, "k": 4096, "m": 1, "group_size": 32,
-                   "weight_copies_rotated": c2["copies"], "timing": "hip graph of K launches"},
+                   "weight_copies_rotated": c2["copies"],
+                   "timing": "one replay of a HIP graph of K launches, queued behind a device spin and an untimed replay; HIP events on the launch stream"},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
                      "traffic": measured_traffic("c2")},
@@ -651,7 +718,8 @@ def main():
             "roofline": {"bound": "mfma", "achieved": round(c4["tflops"], 2),
                          "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s",
                          "frac": round(c4["frac"], 4), "traffic": measured_traffic("c4"),
-                         "mfma_busy": measured_mfma_busy("c4")}},
+                         "mfma_busy": measured_mfma_busy("c4")},
+            "cpu_baseline": cpu4},
         "fp32_gemv_c1": c1,
         "int8_gemm_c3": c3s or None,
         "w4a8_gemm_c5": c5,

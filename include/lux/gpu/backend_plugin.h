@@ -14,8 +14,12 @@
  *   - the device-info fields follow webgpu_get_device_info (:1369-1389);
  *   - the capability bits follow docs/architecture.md:112-123;
  *   - the error names follow every `return LUX_BACKEND_*` in the plugin.  Their
- *     numeric values are not recoverable from the reference; they are assigned
- *     here in the order the public LuxError enum uses (docs/api.md:662-670).
+ *     numeric values are not recoverable from the reference.  OK, INVALID_ARGUMENT
+ *     and OUT_OF_MEMORY take the values of the same-named codes of the public
+ *     LuxError enum (0, 1, 2; docs/api.md:662-670).  NOT_SUPPORTED (3), DEVICE_LOST
+ *     (4) and INTERNAL (5) are numbered here; they do NOT follow LuxError, whose
+ *     NOT_SUPPORTED is 6 and whose 3-5 are BACKEND_NOT_AVAILABLE, DEVICE_NOT_FOUND
+ *     and KERNEL_FAILED.  A core built against the canonical header maps by name.
  * A loader guards against a layout mismatch through `vtbl_size`
  * (src/webgpu_plugin.cpp:4133).
  *

@@ -163,3 +163,72 @@ def test_graph_codecs_and_gemv_forms(plugin):
             prev = got
     finally:
         c.close()
+
+
+def test_graph_survives_workspace_growth(plugin):
+    """A graph captured with the context's workspace keeps replaying correctly after an
+    eager call on the same context grows the workspace: the old block is retired, not
+    freed.  A call inside capture that would need a larger workspace is refused with
+    NOT_SUPPORTED (hipMalloc is not allowed there) and launches nothing."""
+    import torch
+    c = plugin.create_context(0)
+    try:
+        r = rng(4444)
+        m, n, k = 100, 256, 512                       # large-m int4 GEMM: small workspace
+        _, Wl, sl = int4_weights(r, n, k, 32)
+        xl = torch.tensor(r.standard_normal((m, k)), dtype=torch.bfloat16, device="cuda")
+        wl, s_l, xlb = c.upload(Wl), c.upload(sl), c.wrap(xl)
+        d = W.qdesc(n, k, m, 4, 32, 0, W.SCALE_F16, W.BF16, W.BF16)
+        og, oe = c.alloc(m * n * 2), c.alloc(m * n * 2)
+        c.qmatmul(d, wl, s_l, xlb, None, og)          # sizes the workspace eagerly
+        s = torch.cuda.Stream()
+        c.set_stream(s.cuda_stream)
+        c.set_synchronous(False)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            c.qmatmul(d, wl, s_l, xlb, None, og)
+        c.set_stream(None)
+        c.set_synchronous(True)
+
+        # an eager call with a much larger activation block grows the workspace
+        M2, K2 = 2048, 4096
+        _, W2, s2 = int4_weights(r, 256, K2, 32)
+        x2 = torch.tensor(r.standard_normal((M2, K2)), dtype=torch.bfloat16, device="cuda")
+        d2 = W.qdesc(256, K2, M2, 4, 32, 0, W.SCALE_F16, W.BF16, W.BF16)
+        w2, sb2, x2b, y2 = c.upload(W2), c.upload(s2), c.wrap(x2), c.alloc(M2 * 256 * 2)
+        c.qmatmul(d2, w2, sb2, x2b, None, y2)
+        junk = torch.full((64 << 20,), 7, dtype=torch.uint8, device="cuda")  # reuse bait
+        torch.cuda.synchronize()
+
+        for i in range(3):
+            xl.copy_(torch.tensor(r.standard_normal((m, k)), dtype=torch.bfloat16))
+            torch.cuda.synchronize()
+            with torch.cuda.stream(s):
+                g.replay()
+            torch.cuda.synchronize()
+            c.qmatmul(d, wl, s_l, xlb, None, oe)
+            got = c.download(og, np.uint16, (m, n))
+            ref = c.download(oe, np.uint16, (m, n))
+            assert np.array_equal(got, ref), f"replay {i} after workspace growth"
+
+        # growth inside capture: refused, nothing launched
+        M3 = 4096
+        x3 = torch.zeros((M3, K2), dtype=torch.bfloat16, device="cuda")
+        x3b, y3 = c.wrap(x3), c.alloc(M3 * 256 * 2)
+        d3 = W.qdesc(256, K2, M3, 4, 32, 0, W.SCALE_F16, W.BF16, W.BF16)
+        c.set_stream(s.cuda_stream)
+        c.set_synchronous(False)
+        g3 = torch.cuda.CUDAGraph()
+        err = None
+        with torch.cuda.graph(g3, stream=s):
+            c.qmatmul(d, wl, s_l, xlb, None, og)      # fits: captured
+            try:
+                c.qmatmul(d3, w2, sb2, x3b, None, y3)
+            except W.LuxError as e:
+                err = e
+        c.set_stream(None)
+        c.set_synchronous(True)
+        assert err is not None and err.code == W.LUX_BACKEND_ERROR_NOT_SUPPORTED, err
+        del junk
+    finally:
+        c.close()

@@ -182,3 +182,79 @@ def test_int4_wide_range_activations(ctx, m, xd):
     assert np.all(np.isfinite(got))
     for i in range(m):
         compare(got[i], ref[i].astype(np.float64), f"wide-range row {i} m{m} {xd}")
+
+
+# ------------------------------------------------------------------ scale range
+# The reference dequantizes f32(q) * scale in fp32 (quantized_nax.wgsl:589-608), and its
+# producer (compute_group_scales, :157-232) writes fp32 scales of any magnitude.  The m > 1
+# int4 kernels stage q * s as fp16 after dividing each weight row's scales by a power of
+# two (the row's scale fold), so tiny, fp16-subnormal and huge scales must give the
+# oracle's result.  m = 1 is the GEMV (fp32 scales), m = 8 / 64 the small-m MFMA kernel,
+# m = 2048 the large-m MFMA kernel.
+SCALE_RANGES = {"tiny": (1e-9, 1e-7), "f16sub": (2.0 ** -24, 2.0 ** -14), "huge": (1e4, 1e5)}
+
+
+def _scale_buffer(s32, fmt):
+    """Scales in the requested storage and the fp32 values the oracle must use."""
+    if fmt == W.SCALE_F16:
+        s16 = np.minimum(s32, 60000.0).astype(np.float16)
+        return s16, s16.astype(np.float32)
+    if fmt == W.SCALE_F32:
+        return s32, s32
+    gsb = np.zeros(s32.shape + (4,), np.float32)
+    gsb[..., 0] = s32
+    return gsb, s32
+
+
+@pytest.mark.parametrize("rname", list(SCALE_RANGES))
+@pytest.mark.parametrize("fmt", [W.SCALE_F32, W.SCALE_GROUPSCALE, W.SCALE_F16])
+@pytest.mark.parametrize("m", [1, 8, 64, 2048])
+def test_int4_scale_range(ctx, m, fmt, rname):
+    r = rng(1000 + m + 10 * fmt + len(rname))
+    n_out, K, gs = 256, 512, 32
+    q, Wp, _ = int4_weights(r, n_out, K, gs)
+    lo, hi = SCALE_RANGES[rname]
+    sbuf, sref = _scale_buffer(r.uniform(lo, hi, size=(n_out, K // gs)).astype(np.float32), fmt)
+    X, Xf, xc = _x(r, m, K, "bf16" if m == 2048 else "f16")
+    d = W.qdesc(n_out, K, m, 4, gs, W.NIBBLE_OFFSET_BINARY, fmt, xc, W.F32)
+    got = _run(ctx, d, Wp, sbuf, X, n_out, m, "f32")
+    ref = oracle.matmul_nax_grouped_tokens(Wp, sref.reshape(-1), Xf, gs).astype(np.float64)
+    assert np.all(np.isfinite(got))
+    st = compare(got, ref, f"scale range {rname} fmt {fmt} m {m}")
+    for i in range(0, m, max(1, m // 16)):  # token rows
+        compare(got[i], ref[i], f"scale range {rname} fmt {fmt} m {m} token {i}")
+    print(f"scale range {rname} fmt {fmt} m {m}: rel-L2 {st['rel_l2']:.2e}")
+
+
+@pytest.mark.parametrize("fmt", [W.SCALE_F32, W.SCALE_GROUPSCALE])
+@pytest.mark.parametrize("m", [8, 64, 300])
+def test_int4_scales_vary_per_weight_row(ctx, m, fmt):
+    """Each weight row's scales sit at their own magnitude, 10^U(-9, 5): every row gets
+    its own fold; checked weight row by weight row (output column by column)."""
+    r = rng(2000 + m + fmt)
+    n_out, K, gs = 320, 512, 64
+    q, Wp, _ = int4_weights(r, n_out, K, gs)
+    mag = 10.0 ** r.uniform(-9, 5, size=(n_out, 1))
+    s32 = (r.uniform(0.5, 1.0, size=(n_out, K // gs)) * mag).astype(np.float32)
+    sbuf, sref = _scale_buffer(s32, fmt)
+    X, Xf, xc = _x(r, m, K, "bf16")
+    d = W.qdesc(n_out, K, m, 4, gs, W.NIBBLE_OFFSET_BINARY, fmt, xc, W.F32)
+    got = _run(ctx, d, Wp, sbuf, X, n_out, m, "f32")
+    ref = oracle.matmul_nax_grouped_tokens(Wp, sref.reshape(-1), Xf, gs).astype(np.float64)
+    for n in range(n_out):
+        compare(got[:, n], ref[:, n], f"per-row magnitude m {m} fmt {fmt} weight row {n}")
+
+
+@pytest.mark.parametrize("fmt", [W.SCALE_F32, W.SCALE_GROUPSCALE])
+@pytest.mark.parametrize("coding", [0, 1])
+def test_int4_small_m_formats(ctx, fmt, coding):
+    """The small-m kernel with fp32 and GroupScale scales, both nibble codings."""
+    r = rng(60 + 2 * fmt + coding)
+    n_out, K, m, gs = 384, 512, 24, 64
+    q, Wp, _ = int4_weights(r, n_out, K, gs, coding)
+    sbuf, sref = _scale_buffer(r.uniform(0.005, 0.02, size=(n_out, K // gs)).astype(np.float32), fmt)
+    X, Xf, xc = _x(r, m, K, "f16")
+    d = W.qdesc(n_out, K, m, 4, gs, coding, fmt, xc, W.F16)
+    got = _run(ctx, d, Wp, sbuf, X, n_out, m, "f16")
+    ref = oracle.matmul_nax_grouped_tokens(Wp, sref.reshape(-1), Xf, gs, coding)
+    compare(got, round_to(ref, "f16"), f"small-m formats {fmt} {coding}")

@@ -148,6 +148,59 @@ __device__ __forceinline__ float row_pow2_factor(uint32_t mx, int mant) {
     return ldexpf(1.0f, max(ex - 141, -126));
 }
 
+// ---- fp16 staging of dequantised int4 weights ------------------------------------
+// Kernels that stage q * s as fp16 for fp16 MFMAs (q in [-8, 7]) first divide the scales
+// of each weight row by a power of two, fold = 2^(E - 11) with 2^E <= max_g |s(n, g)| <
+// 2^(E+1): the row's largest |s / fold| lies in [2^11, 2^12), so |q * s / fold| <= 2^15
+// stays inside fp16's normal range for any finite scale (fp32 scales of any exponent,
+// fp16 scales up to 65504), and groups down to 2^-25 of the row maximum keep full fp16
+// precision.  The product is rounded to fp16 once; the epilogue multiplies the row's
+// fp32 sum by fold (exact).  Rows whose scales are all zero, or hold Inf/NaN, keep
+// fold = 1 (Inf/NaN then propagate as in the reference's f32(q) * s).  `mx` is the
+// largest |s| of the row as binary32 bits (sign cleared).
+__device__ __forceinline__ float scale_fold_factor(uint32_t mx) {
+    if (mx == 0 || mx >= 0x7F800000u) return 1.0f;
+    const int ex = (int)(mx >> 23);  // 0 for a binary32 subnormal maximum
+    return ldexpf(1.0f, max(ex - 127 - 11, -126));
+}
+
+// |s| as binary32 bits from a raw scale word of load_scale_raw.
+template <ScaleKind K>
+__device__ __forceinline__ uint32_t scale_abs_bits(uint32_t raw) {
+    return __builtin_bit_cast(uint32_t, scale_from_raw<K>(raw)) & 0x7FFFFFFFu;
+}
+
+// fold[row] of the G scales of one weight row, computed by one wave.
+template <ScaleKind K>
+__device__ __forceinline__ float row_scale_fold(const void* s, size_t row, int G, int lane) {
+    uint32_t mx = 0;
+    int g = lane;
+    for (; g + 192 < G; g += 256) {  // four independent loads per lane per trip
+        const uint32_t a = load_scale_raw<K>(s, row * G + g), b = load_scale_raw<K>(s, row * G + g + 64);
+        const uint32_t c = load_scale_raw<K>(s, row * G + g + 128), d = load_scale_raw<K>(s, row * G + g + 192);
+        mx = max(mx, max(max(scale_abs_bits<K>(a), scale_abs_bits<K>(b)), max(scale_abs_bits<K>(c), scale_abs_bits<K>(d))));
+    }
+    for (; g < G; g += 64) mx = max(mx, scale_abs_bits<K>(load_scale_raw<K>(s, row * G + g)));
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) mx = max(mx, (uint32_t)__shfl_xor((int)mx, o, 64));
+    // A NaN scale compares above every finite value and Inf as bits, so it also keeps fold = 1.
+    return scale_fold_factor(mx);
+}
+
+// Product q * s in fp32 (exact to binary32 rounding), then one RNE rounding to fp16, for
+// one u32 of 8 offset-binary nibbles (k .. k+7), in the staging order
+// (k, k+4, k+1, k+5, k+2, k+6, k+3, k+7).
+__device__ __forceinline__ u32x4 dequant8_f32s(uint32_t w, float s) {
+    uint32_t o[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const float a = (float)((int)((w >> (4 * i)) & 0xFu) - 8) * s;
+        const float b = (float)((int)((w >> (4 * i + 16)) & 0xFu) - 8) * s;
+        o[i] = __builtin_bit_cast(uint32_t, f16x2{(f16)a, (f16)b});
+    }
+    return u32x4{o[0], o[1], o[2], o[3]};
+}
+
 // Block-wide max of a per-thread value; `red` is __shared__ scratch of >= 16 words.
 __device__ __forceinline__ uint32_t block_max_u32(uint32_t v, uint32_t* red) {
 #pragma unroll
@@ -198,6 +251,7 @@ struct QArgs {
     int wbits;            // 4 or 8
     uint32_t xor_mask;    // 0x88888888 turns two's-complement nibbles into offset-binary
     const float* xfac;    // per-row power-of-two factors of staged activations (set by launchers)
+    const float* wfold;   // per-weight-row scale folds of fp16-staged int4 weights (set by launchers)
     ScaleKind scale_kind;
     XKind x_kind;
     YKind y_kind;
@@ -223,9 +277,13 @@ hipError_t launch_gemv_f16(const void* A, const void* x, float* y, int M, int K,
 // int4 weight-only GEMV, m == 1.
 bool qgemv_i4_fast(const QArgs& a);  // the m = 1 int4 GEMV fast path applies (SiluMul needs it)
 hipError_t launch_qgemv_i4(const QArgs& a, hipStream_t s);
+// Per-weight-row scale folds (scale_fold_factor) of int4 weights staged as fp16:
+// fold[n] for n < n_out, one wave per row.
+hipError_t launch_scale_fold(const void* s, ScaleKind sk, int n_out, int groups, float* fold, hipStream_t st);
 // Weight-only int4/int8 matmul for small m (bandwidth regime), fp16/bf16/f32 X.
 bool qgemm_small_supported(const QArgs& a);
-// workspace: qgemm_small_workspace(a) bytes (per-row activation factors; 0 for fp16 X)
+// workspace: qgemm_small_workspace(a) bytes (int4: per-row scale folds; bf16/f32 X:
+// per-row activation factors; 0 for int8 weights with fp16 X), 16-byte aligned
 size_t qgemm_small_workspace(const QArgs& a);
 hipError_t launch_qgemm_small(const QArgs& a, void* workspace, hipStream_t s);
 // int4 grouped GEMM for large m (MFMA regime).  Needs a device workspace of

@@ -22,6 +22,7 @@
 #include <cstring>
 #include <string>
 #include <thread>
+#include <vector>
 
 #include "common.hpp"
 #include "lux/gpu/backend_plugin.h"
@@ -55,27 +56,44 @@ struct HipCtx {
     std::string name;
     std::string force_fail;  // LUX_HIP_FORCE_FAIL test hook: op name that fails
     hipDeviceProp_t props{};
-    void* ws = nullptr;      // device workspace (staged activations), grown on demand
+    void* ws = nullptr;      // device workspace (staged activations, partial sums), grown on demand
     size_t ws_size = 0;
+    // Workspaces replaced by a larger one.  They stay allocated until destroy_context: a
+    // HIP graph captured earlier on this context still holds their addresses.  Growth is
+    // at least 2x, so the retired blocks together are smaller than the current one.
+    std::vector<void*> ws_retired;
 };
 
-// Workspace of at least `bytes` on the context's device.  Growing it waits for the
-// stream (the old block may still be in use) and calls hipMalloc, so the first call
-// of a shape must not happen inside stream capture.
-void* ensure_workspace(HipCtx* c, size_t bytes) {
-    if (bytes <= c->ws_size) return c->ws;
-    (void)hipStreamSynchronize(c->stream);
-    if (c->ws) (void)hipFree(c->ws);
-    c->ws = nullptr;
-    c->ws_size = 0;
-    const size_t sz = (bytes + 0xFFFFF) & ~(size_t)0xFFFFF;  // 1 MiB granules
-    if (hipMalloc(&c->ws, sz) != hipSuccess) {
-        (void)hipGetLastError();
-        c->ws = nullptr;
-        return nullptr;
+// Workspace of at least `bytes` on the context's device, in *out.  Growing it calls
+// hipMalloc, which stream capture does not allow: a call inside capture that needs a
+// larger workspace returns NOT_SUPPORTED (run the shape once eagerly before capturing).
+// The old block is kept (not freed), so graphs captured before the growth replay
+// unchanged.  Every op of a context shares the one workspace, so work on one context must
+// not run concurrently with itself (graph replays included).
+LuxBackendError get_workspace(HipCtx* c, size_t bytes, void** out, const char* op) {
+    *out = nullptr;
+    if (bytes <= c->ws_size) {
+        *out = c->ws;
+        return LUX_BACKEND_OK;
     }
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(c->stream, &cs) != hipSuccess) (void)hipGetLastError();
+    if (cs != hipStreamCaptureStatusNone)
+        return fail(LUX_BACKEND_ERROR_NOT_SUPPORTED,
+                    "%s: workspace must grow to %zu bytes during stream capture; run this shape once "
+                    "eagerly before capturing", op, bytes);
+    size_t sz = std::max(bytes, 2 * c->ws_size);
+    sz = (sz + 0xFFFFF) & ~(size_t)0xFFFFF;  // 1 MiB granules
+    void* p = nullptr;
+    if (hipMalloc(&p, sz) != hipSuccess) {
+        (void)hipGetLastError();
+        return fail(LUX_BACKEND_ERROR_OUT_OF_MEMORY, "%s: workspace allocation of %zu bytes failed", op, sz);
+    }
+    if (c->ws) c->ws_retired.push_back(c->ws);
+    c->ws = p;
     c->ws_size = sz;
-    return c->ws;
+    *out = p;
+    return LUX_BACKEND_OK;
 }
 
 struct HipBuf {
@@ -169,6 +187,7 @@ void hip_destroy_context(LuxBackendContext* ctx) {
         (void)hipStreamDestroy(c->own_stream);
     }
     if (c->ws) (void)hipFree(c->ws);
+    for (void* p : c->ws_retired) (void)hipFree(p);
     delete c;
 }
 
@@ -307,9 +326,9 @@ LuxBackendError hip_op_matmul_f32(LuxBackendContext* ctx, LuxBackendBuffer* a, L
         he = launch_gemv_f32(pa, pb, po, M, K, K, 1.0f, 0.0f, c->stream);
     } else if (M == 1) {
         // Row vector: C[N] = B^T[N x K] . a[K].
-        float* ws = static_cast<float*>(ensure_workspace(c, gemv_t_workspace(K, N)));
-        if (!ws) return fail(LUX_BACKEND_ERROR_OUT_OF_MEMORY, "op_matmul_f32: workspace allocation failed");
-        he = launch_gemv_f32_t(pb, pa, po, K, N, N, 1.0f, 0.0f, ws, c->stream);
+        void* ws = nullptr;
+        if (LuxBackendError e = get_workspace(c, gemv_t_workspace(K, N), &ws, "op_matmul_f32")) return e;
+        he = launch_gemv_f32_t(pb, pa, po, K, N, N, 1.0f, 0.0f, static_cast<float*>(ws), c->stream);
     } else {
         he = launch_gemm_f32(pa, pb, po, M, K, N, c->stream);
     }
@@ -463,10 +482,10 @@ LUX_EXPORT LuxBackendError lux_hip_gemv_f32(LuxBackendContext* ctx, LuxBackendBu
     if (outn == 0) return LUX_BACKEND_OK;
     hipError_t he;
     if (p->trans) {
-        float* ws = static_cast<float*>(ensure_workspace(c, gemv_t_workspace((int)M, (int)N)));
-        if (!ws) return fail(LUX_BACKEND_ERROR_OUT_OF_MEMORY, "gemv_f32: workspace allocation failed");
+        void* ws = nullptr;
+        if (LuxBackendError e = get_workspace(c, gemv_t_workspace((int)M, (int)N), &ws, "gemv_f32")) return e;
         he = launch_gemv_f32_t((const float*)A->ptr, (const float*)X->ptr, (float*)Y->ptr, (int)M, (int)N,
-                               (int)lda, p->alpha, p->beta, ws, c->stream);
+                               (int)lda, p->alpha, p->beta, static_cast<float*>(ws), c->stream);
     }
     else {
         he = launch_gemv_f32((const float*)A->ptr, (const float*)X->ptr, (float*)Y->ptr, (int)M, (int)N,
@@ -598,6 +617,19 @@ LuxBackendError qmatmul_impl(LuxBackendContext* ctx, const LuxHipQMatmulDesc* d,
     const bool need_xs = w4a8 && d->y_dtype != LUX_HIP_I32 && !qx;
     if (need_xs && !fits(XS, (size_t)M * 4))
         return fail(LUX_BACKEND_ERROR_INVALID_ARGUMENT, "qmatmul: x_scales (f32 [m]) required for W4A8 fp output");
+    // Natural alignment of every element type (wrapped views may start anywhere); the
+    // kernels' 16-byte vector paths check their own stronger requirements and fall back
+    // or refuse.  QUANTIZE_X reads x with 16-byte loads.
+    {
+        const uintptr_t wa = (uintptr_t)W->ptr, xa = (uintptr_t)X->ptr, ya = (uintptr_t)Y->ptr;
+        const uintptr_t sa = no_scale ? 0 : (uintptr_t)S->ptr;
+        const size_t sal = no_scale ? 1 : std::min<size_t>(scale_bytes(d->scale_format), 4);
+        if ((d->weight_bits == 4 && (wa & 3u)) || (sa & (sal - 1)) || (xa & (xb - 1)) || (ya & (yb - 1)) ||
+            (qx && (xa & 15u)) || (need_xs && ((uintptr_t)XS->ptr & 3u)))
+            return fail(LUX_BACKEND_ERROR_NOT_SUPPORTED,
+                        "qmatmul: misaligned buffer (w, scales, x or y not naturally aligned, or x not 16-byte "
+                        "aligned for QUANTIZE_X)");
+    }
 
     if (LuxBackendError e = begin_op(c, "qmatmul")) return e;
     if (M == 0 || n_out == 0) return LUX_BACKEND_OK;
@@ -628,8 +660,9 @@ LuxBackendError qmatmul_impl(LuxBackendContext* ctx, const LuxHipQMatmulDesc* d,
     if (w4a8) {
         if (qx) {  // int8 activations and their f32 per-token scales in the workspace
             a.x_kind = XKind::I8;
-            uint8_t* ws = static_cast<uint8_t*>(ensure_workspace(c, (size_t)M * K + (size_t)M * 4));
-            if (!ws) return fail(LUX_BACKEND_ERROR_OUT_OF_MEMORY, "qmatmul: workspace allocation failed");
+            void* wsv = nullptr;
+            if (LuxBackendError e = get_workspace(c, (size_t)M * K + (size_t)M * 4, &wsv, "qmatmul")) return e;
+            uint8_t* ws = static_cast<uint8_t*>(wsv);
             a.x = ws;
             a.xs = reinterpret_cast<const float*>(ws + (size_t)M * K);
             if (!w4a8_supported(a))
@@ -656,17 +689,19 @@ LuxBackendError qmatmul_impl(LuxBackendContext* ctx, const LuxHipQMatmulDesc* d,
     } else if (M <= 64 && qgemm_small_supported(a)) {
         // decode batches: bandwidth regime, weights streamed once per 64 tokens
         const size_t wsb = qgemm_small_workspace(a);
-        void* ws = wsb ? ensure_workspace(c, wsb) : nullptr;
-        if (wsb && !ws) return fail(LUX_BACKEND_ERROR_OUT_OF_MEMORY, "qmatmul: workspace allocation failed");
+        void* ws = nullptr;
+        if (wsb)
+            if (LuxBackendError e = get_workspace(c, wsb, &ws, "qmatmul")) return e;
         he = launch_qgemm_small(a, ws, c->stream);
     } else if (d->weight_bits == 4 && qgemm_i4_large_supported(a)) {
-        void* ws = ensure_workspace(c, qgemm_i4_large_workspace(a));
-        if (!ws) return fail(LUX_BACKEND_ERROR_OUT_OF_MEMORY, "qmatmul: workspace allocation failed");
+        void* ws = nullptr;
+        if (LuxBackendError e = get_workspace(c, qgemm_i4_large_workspace(a), &ws, "qmatmul")) return e;
         he = launch_qgemm_i4_large(a, ws, c->stream);
     } else if (qgemm_small_supported(a)) {
         const size_t wsb = qgemm_small_workspace(a);
-        void* ws = wsb ? ensure_workspace(c, wsb) : nullptr;
-        if (wsb && !ws) return fail(LUX_BACKEND_ERROR_OUT_OF_MEMORY, "qmatmul: workspace allocation failed");
+        void* ws = nullptr;
+        if (wsb)
+            if (LuxBackendError e = get_workspace(c, wsb, &ws, "qmatmul")) return e;
         he = launch_qgemm_small(a, ws, c->stream);
     } else {
         return fail(LUX_BACKEND_ERROR_NOT_SUPPORTED, "qmatmul: no kernel for this descriptor");

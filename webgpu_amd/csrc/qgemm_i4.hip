@@ -9,9 +9,12 @@
 // Numerics: X (bf16) is staged as fp16 after dividing each row by a power of two
 // that puts its largest |x| in [2^14, 2^15); bf16 carries 8 significant bits and fp16
 // 11, so the staging is exact for every element within 2^-28 of the row maximum and
-// cannot overflow.  The epilogue multiplies the row back (exact).  The dequantised weight q*s is
-// staged as fp16 rounded to nearest-even: the exact product needs up to 14
-// significant bits, so each staged weight carries a relative error <= 2^-11.
+// cannot overflow.  The epilogue multiplies the row back (exact).  The dequantised weight
+// q*s/fold is staged as fp16 rounded to nearest-even, fold being the weight row's
+// power-of-two scale fold (scale_fold_factor, computed by the pre-pass), which the
+// epilogue multiplies back: any finite fp16 / fp32 / GroupScale scale stays in fp16's
+// normal range.  The exact product needs up to 14 significant bits (more for fp32
+// scales), so each staged weight carries one rounding, a relative error <= 2^-11.
 // Products are exact in the MFMA and accumulate in fp32.  Against the
 // fp32 oracle rounded to bf16 this measures rel-L2 ~8e-4 on config 4, inside
 // the stated 1e-3 (the bf16 output rounding alone is worth 1.7e-3 against the
@@ -62,18 +65,6 @@ __device__ __forceinline__ u32x4 dequant8(uint32_t w, f16x2 s2, uint32_t magic) 
     return u32x4{o[0], o[1], o[2], o[3]};
 }
 
-// Same with an fp32 scale: product in fp32 (exact), then RNE to fp16; staging order.
-__device__ __forceinline__ u32x4 dequant8_f32(uint32_t w, float s) {
-    uint32_t o[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const float a = (float)((int)((w >> (4 * i)) & 0xFu) - 8) * s;
-        const float b = (float)((int)((w >> (4 * i + 16)) & 0xFu) - 8) * s;
-        o[i] = pack_h2((f16)a, (f16)b);
-    }
-    return u32x4{o[0], o[1], o[2], o[3]};
-}
-
 }  // namespace
 
 // X -> fp16 in staging order.  Runs once per call ahead of the GEMM, so each
@@ -101,11 +92,23 @@ __device__ __forceinline__ u32x4 bf16x8_to_staged_f16(u32x4 v, float inv) {
     return u32x4{pack_h2(h[0], h[4]), pack_h2(h[1], h[5]), pack_h2(h[2], h[6]), pack_h2(h[3], h[7])};
 }
 
-template <XKind XK>
+// Blocks past the first ceil(M / 4) compute the weight rows' scale folds instead (one
+// wave per weight row, row_scale_fold), so one launch prepares both operands.
+template <XKind XK, ScaleKind SK>
 __global__ __launch_bounds__(256) void k_x_to_f16_rows(const void* __restrict__ X,
                                                        u32x4* __restrict__ out,
-                                                       float* __restrict__ fac, int M, int K) {
+                                                       float* __restrict__ fac, int M, int K,
+                                                       const void* __restrict__ S, float* __restrict__ wfold,
+                                                       int N, int G) {
     const int lane = threadIdx.x & 63;
+    const int xblocks = (M + 3) / 4;
+    if ((int)blockIdx.x >= xblocks) {
+        const int wrow = ((int)blockIdx.x - xblocks) * 4 + (threadIdx.x >> 6);
+        if (wrow >= N) return;
+        const float f = row_scale_fold<SK>(S, (size_t)wrow, G, lane);
+        if (lane == 0) wfold[wrow] = f;
+        return;
+    }
     const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (row >= M) return;
     const int n8 = K / 8;
@@ -150,7 +153,8 @@ __global__ __launch_bounds__(256) void k_x_to_f16_rows(const void* __restrict__ 
 template <ScaleKind SK, YKind YK>
 __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void k_qgemm_i4_large(const f16* __restrict__ X, const float* __restrict__ xfac,
-                      const uint32_t* __restrict__ W, const void* __restrict__ S, void* __restrict__ Y,
+                      const uint32_t* __restrict__ W, const void* __restrict__ S,
+                      const float* __restrict__ wfold, void* __restrict__ Y,
                       int M, int N, int K, int gs, uint32_t xor_mask, int vec_y, EpiArgs epi) {
     extern __shared__ __attribute__((aligned(16))) f16 lds[];
     f16* xs = lds;                          // [2][BM][LDS_ROW]
@@ -194,6 +198,7 @@ void k_qgemm_i4_large(const f16* __restrict__ X, const float* __restrict__ xfac,
     const int wgr = grow(wr_row);
     const uint32_t woff = wgr >= 0 ? (uint32_t)((size_t)wgr * (K / 2) + 16 * wh) : wbytes;
     const int srow = wgr >= 0 ? wgr : N - 1;
+    const float winv = 1.0f / wfold[srow];  // exact: the fold is a power of two
     const uint32_t magic = 0x64006400u;
 
     // Staging registers, two sets: the data of stage t is loaded during stage t-2 and
@@ -218,16 +223,17 @@ void k_qgemm_i4_large(const f16* __restrict__ X, const float* __restrict__ xfac,
         f16* wb = ws + buf * BN * LDS_ROW + wr_row * LDS_ROW + 32 * wh;
         const uint32_t words[4] = {R.wr.x, R.wr.y, R.wr.z, R.wr.w};
         if constexpr (SK == ScaleKind::F16) {
-            const f16 sc = __builtin_bit_cast(f16, (uint16_t)R.sr);
+            // an fp16 scale times a power of two is exact in fp16: q * s rounds once
+            const f16 sc = (f16)(scale_from_raw<SK>(R.sr) * winv);
             const f16x2 s2 = {sc, sc};
 #pragma unroll
             for (int q = 0; q < 4; ++q)
                 *reinterpret_cast<u32x4*>(wb + 8 * q) = dequant8(words[q] ^ xor_mask, s2, magic);
         } else {
-            const float sc = scale_from_raw<SK>(R.sr);
+            const float sc = scale_from_raw<SK>(R.sr) * winv;
 #pragma unroll
             for (int q = 0; q < 4; ++q)
-                *reinterpret_cast<u32x4*>(wb + 8 * q) = dequant8_f32(words[q] ^ xor_mask, sc);
+                *reinterpret_cast<u32x4*>(wb + 8 * q) = dequant8_f32s(words[q] ^ xor_mask, sc);
         }
     };
 
@@ -297,10 +303,16 @@ void k_qgemm_i4_large(const f16* __restrict__ X, const float* __restrict__ xfac,
     }
     if (nstages & 1) compute(0, R1);
 
-    // The block's 256 row factors of X (fp32) go to the now idle LDS, once.
+    // The block's 256 row factors of X and the scale folds of its 256 weight rows (fp32,
+    // by LDS row of the weight tile) go to the now idle LDS, once.
     __syncthreads();
     float* fac = reinterpret_cast<float*>(lds);
+    float* wf = fac + BM;
     if (tid < BM) fac[tid] = m0 + tid < M ? xfac[m0 + tid] : 0.0f;
+    else if (tid < BM + BN) {
+        const int g = grow(tid - BM);
+        wf[tid - BM] = g >= 0 ? wfold[g] : 1.0f;
+    }
     __syncthreads();
 
     // Epilogue: D[r][c] of a 32x32 tile (r = weight row, c = activation row) sits in
@@ -319,7 +331,10 @@ void k_qgemm_i4_large(const f16* __restrict__ X, const float* __restrict__ xfac,
                 const int n = g0 + wn * 32 + 8 * g + 4 * (lane >> 5);
                 f32x4 v;
 #pragma unroll
-                for (int r = 0; r < 4; ++r) v[r] = silu_f(acc[0][i][4 * g + r] * fm) * (acc[1][i][4 * g + r] * fm);
+                for (int r = 0; r < 4; ++r) {
+                    const int rho = wn * 64 + 8 * g + 4 * (lane >> 5) + r;  // gate row; its up row is rho + 32
+                    v[r] = silu_f(acc[0][i][4 * g + r] * fm * wf[rho]) * (acc[1][i][4 * g + r] * fm * wf[rho + 32]);
+                }
                 if (vec && n + 3 < nh) {
                     store_y4<YK>(Y, (size_t)m * nh + n, v);
                 } else {
@@ -335,8 +350,9 @@ void k_qgemm_i4_large(const f16* __restrict__ X, const float* __restrict__ xfac,
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
                 const int n = n0 + wn * 64 + 32 * j + 8 * g + 4 * (lane >> 5);
-                f32x4 v = f32x4{acc[j][i][4 * g], acc[j][i][4 * g + 1], acc[j][i][4 * g + 2],
-                                acc[j][i][4 * g + 3]} * fm;
+                const int rho = wn * 64 + 32 * j + 8 * g + 4 * (lane >> 5);
+                f32x4 v = f32x4{acc[j][i][4 * g] * wf[rho], acc[j][i][4 * g + 1] * wf[rho + 1],
+                                acc[j][i][4 * g + 2] * wf[rho + 2], acc[j][i][4 * g + 3] * wf[rho + 3]} * fm;
                 if (epi.kind != 0) {
 #pragma unroll
                     for (int r = 0; r < 4; ++r) v[r] = apply_epi(v[r], epi, m, min(n + r, N - 1), N);
@@ -362,7 +378,7 @@ bool qgemm_i4_large_supported(const QArgs& a) {
 }
 
 template <ScaleKind SK, YKind YK>
-static void launch_t(const QArgs& a, const f16* xst, const float* xfac, hipStream_t s) {
+static void launch_t(const QArgs& a, const f16* xst, const float* xfac, const float* wfold, hipStream_t s) {
     const bool sm = a.epi.kind == (int)Epi::SiluMul;
     const int ny = sm ? a.n_out / 2 : a.n_out;  // output columns
     const dim3 grid(sm ? (ny + BN / 2 - 1) / (BN / 2) : (a.n_out + BN - 1) / BN, (a.m + BM - 1) / BM), block(NT);
@@ -374,41 +390,46 @@ static void launch_t(const QArgs& a, const f16* xst, const float* xfac, hipStrea
     }();
     (void)attr;
     hipLaunchKernelGGL((k_qgemm_i4_large<SK, YK>), grid, block, lds, s, xst, xfac,
-                       reinterpret_cast<const uint32_t*>(a.w), a.s, a.y, a.m, a.n_out, a.k,
+                       reinterpret_cast<const uint32_t*>(a.w), a.s, wfold, a.y, a.m, a.n_out, a.k,
                        a.group_size, a.xor_mask,
                        (ny % 4 == 0 && ((uintptr_t)a.y & 15u) == 0) ? 1 : 0, a.epi);
 }
 
 template <ScaleKind SK>
-static bool launch_y(const QArgs& a, const f16* xst, const float* xfac, hipStream_t s) {
+static bool launch_y(const QArgs& a, u32x4* xst, float* xfac, float* wfold, hipStream_t s) {
+    // pre-pass: X rows to fp16 and the weight rows' scale folds, one launch
+    const dim3 pgrid((a.m + 3) / 4 + (a.n_out + 3) / 4), pblock(256);
+    const int G = a.k / a.group_size;
+    if (a.x_kind == XKind::BF16)
+        hipLaunchKernelGGL((k_x_to_f16_rows<XKind::BF16, SK>), pgrid, pblock, 0, s, a.x, xst, xfac, a.m, a.k, a.s,
+                           wfold, a.n_out, G);
+    else
+        hipLaunchKernelGGL((k_x_to_f16_rows<XKind::F16, SK>), pgrid, pblock, 0, s, a.x, xst, xfac, a.m, a.k, a.s,
+                           wfold, a.n_out, G);
+    const f16* xh = reinterpret_cast<const f16*>(xst);
     switch (a.y_kind) {
-        case YKind::F32: launch_t<SK, YKind::F32>(a, xst, xfac, s); return true;
-        case YKind::F16: launch_t<SK, YKind::F16>(a, xst, xfac, s); return true;
-        case YKind::BF16: launch_t<SK, YKind::BF16>(a, xst, xfac, s); return true;
+        case YKind::F32: launch_t<SK, YKind::F32>(a, xh, xfac, wfold, s); return true;
+        case YKind::F16: launch_t<SK, YKind::F16>(a, xh, xfac, wfold, s); return true;
+        case YKind::BF16: launch_t<SK, YKind::BF16>(a, xh, xfac, wfold, s); return true;
         default: return false;
     }
 }
 
 size_t qgemm_i4_large_workspace(const QArgs& a) {
-    // staged X (fp16) followed by the per-row factors (fp32); k % 64 keeps both aligned
-    return (size_t)a.m * a.k * sizeof(f16) + (size_t)a.m * sizeof(float);
+    // staged X (fp16), the per-row factors of X (fp32), the weight rows' scale folds
+    // (fp32); k % 64 keeps every part aligned
+    return (size_t)a.m * a.k * sizeof(f16) + (size_t)a.m * sizeof(float) + (size_t)a.n_out * sizeof(float);
 }
 
 hipError_t launch_qgemm_i4_large(const QArgs& a, void* workspace, hipStream_t s) {
     u32x4* xst = reinterpret_cast<u32x4*>(workspace);
     float* xfac = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + (size_t)a.m * a.k * sizeof(f16));
-    if (a.x_kind == XKind::BF16)
-        hipLaunchKernelGGL(k_x_to_f16_rows<XKind::BF16>, dim3((a.m + 3) / 4), dim3(256), 0, s, a.x, xst, xfac,
-                           a.m, a.k);
-    else
-        hipLaunchKernelGGL(k_x_to_f16_rows<XKind::F16>, dim3((a.m + 3) / 4), dim3(256), 0, s, a.x, xst, xfac,
-                           a.m, a.k);
-    const f16* xh = reinterpret_cast<const f16*>(workspace);
+    float* wfold = xfac + a.m;
     bool ok = false;
     switch (a.scale_kind) {
-        case ScaleKind::F16: ok = launch_y<ScaleKind::F16>(a, xh, xfac, s); break;
-        case ScaleKind::F32: ok = launch_y<ScaleKind::F32>(a, xh, xfac, s); break;
-        case ScaleKind::GroupScale: ok = launch_y<ScaleKind::GroupScale>(a, xh, xfac, s); break;
+        case ScaleKind::F16: ok = launch_y<ScaleKind::F16>(a, xst, xfac, wfold, s); break;
+        case ScaleKind::F32: ok = launch_y<ScaleKind::F32>(a, xst, xfac, wfold, s); break;
+        case ScaleKind::GroupScale: ok = launch_y<ScaleKind::GroupScale>(a, xst, xfac, wfold, s); break;
         default: break;
     }
     if (!ok) return hipErrorInvalidValue;

@@ -12,7 +12,9 @@
 // MFMA product is exact; the row scale multiplies the fp32 sum at the end (per-group
 // scales multiply fp32 partial sums), which reassociates the reference's
 // sum of (q*s)*x without extra rounding of the weights.  int4 weights are staged as
-// fp16(q*s) (RNE, relative error <= 2^-11), as in the large-m GEMM.
+// fp16(q*s/fold) with one RNE rounding (relative error <= 2^-11), fold being the
+// weight row's power-of-two scale fold (scale_fold_factor), which the epilogue
+// multiplies back: any finite fp16 / fp32 / GroupScale scale stays in range.
 //
 // Layout (gfx950, v_mfma_f32_16x16x32_f16): A = W rows (16 per wave), B = X^T (16 tokens
 // per m-tile).  Lane l owns weight row l % 16 and k-quarter l / 16: each lane streams
@@ -76,7 +78,7 @@ template <int WB, int MT, bool PERROW, ScaleKind SK, XKind XK, YKind YK>
 __global__ __launch_bounds__(64 * MAXW) void k_qgemm_small(
     const uint8_t* __restrict__ W, const void* __restrict__ S, const void* __restrict__ X,
     void* __restrict__ Y, int M, int N, int K, int gs, uint32_t xor_mask, const float* __restrict__ xfac,
-    EpiArgs epi) {
+    const float* __restrict__ wfold, EpiArgs epi) {
     __shared__ __attribute__((aligned(16))) f16 xs[2][16 * MT][XROW];
 
     const int nw = blockDim.x >> 6;
@@ -178,6 +180,9 @@ __global__ __launch_bounds__(64 * MAXW) void k_qgemm_small(
     constexpr int LPC = KC / KPL;              // loads per X chunk
     constexpr int SPLD = WB == 8 ? (PERROW ? 0 : 4) : 1;  // scales per load per lane
     const int row = wrow_of(r16);
+    // int4: 1 / fold of this lane's weight row (a power of two, so the division is exact)
+    float winv = 1.0f;
+    if constexpr (WB == 4) winv = 1.0f / wfold[row];
     const size_t rowbytes = (size_t)K * WB / 8;
     const uint8_t* wrow = W + (size_t)row * rowbytes + 16 * kq;
 
@@ -228,11 +233,19 @@ __global__ __launch_bounds__(64 * MAXW) void k_qgemm_small(
                 for (int r = 0; r < (SPLD > 0 ? SPLD : 1); ++r) sc[l][r] = sq[slot][l][r];
             } else {
                 // four k-steps of 32: word w covers k 32 kq + 8 w .. + 7 of this load
-                const f16 s16 = (f16)scale_from_raw<SK>(sq[slot][l][0]);
-                const f16x2 s2 = {s16, s16};
+                const float sf = scale_from_raw<SK>(sq[slot][l][0]) * winv;
                 const uint32_t words[4] = {q.x, q.y, q.z, q.w};
+                if constexpr (SK == ScaleKind::F16) {
+                    // an fp16 scale times a power of two is exact in fp16: q * s rounds once
+                    const f16 s16 = (f16)sf;
+                    const f16x2 s2 = {s16, s16};
 #pragma unroll
-                for (int st = 0; st < 4; ++st) av[l][st] = i4x8_to_f16(words[st] ^ xor_mask, s2, magic);
+                    for (int st = 0; st < 4; ++st) av[l][st] = i4x8_to_f16(words[st] ^ xor_mask, s2, magic);
+                } else {
+#pragma unroll
+                    for (int st = 0; st < 4; ++st)
+                        av[l][st] = __builtin_bit_cast(f16x8, dequant8_f32s(words[st] ^ xor_mask, sf));
+                }
             }
         }
         load_w(slot, next);
@@ -298,6 +311,11 @@ __global__ __launch_bounds__(64 * MAXW) void k_qgemm_small(
 
     // ---- epilogue: D[i][j] of a 16x16 tile sits in lane j + 16 * (i / 4), register i % 4;
     // i = weight row (n), j = token (m).  The scalings, then the output epilogue.
+    float wf[4] = {1.0f, 1.0f, 1.0f, 1.0f};  // int4: scale folds of rows 4 kq .. 4 kq + 3
+    if constexpr (WB == 4) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) wf[r] = wfold[wrow_of(4 * kq + r)];
+    }
 #pragma unroll
     for (int t = 0; t < MT; ++t) {
         const int m = 16 * t + r16;
@@ -306,6 +324,7 @@ __global__ __launch_bounds__(64 * MAXW) void k_qgemm_small(
             const int i = 4 * kq + r;
             float v = acc[t][r];
             if constexpr (WB == 8 && PERROW) v *= load_scale_t<SK>(S, (size_t)wrow_of(i));
+            if constexpr (WB == 4) v *= wf[r];
             if constexpr (XK != XKind::F16) v *= sfac[m];
             if (sm) {
                 const float up = __shfl_xor(v, 32, 64);  // tile row i + 8 of the same token
@@ -321,7 +340,8 @@ __global__ __launch_bounds__(64 * MAXW) void k_qgemm_small(
 
 bool qgemm_small_supported(const QArgs& a) {
     if (a.x_kind == XKind::I8 || a.y_kind == YKind::I32) return false;
-    if (a.k % KC != 0 || ((uintptr_t)a.w & 15u) != 0) return false;
+    // weights and activations are read with 16-byte vector loads
+    if (a.k % KC != 0 || ((uintptr_t)a.w & 15u) != 0 || ((uintptr_t)a.x & 15u) != 0) return false;
     if (a.wbits == 8) {
         const bool perrow = a.group_size == a.k || a.scale_kind == ScaleKind::None;
         return perrow || a.group_size % 64 == 0;
@@ -349,7 +369,7 @@ static void launch_one(const QArgs& a, const void* x, void* y, const float* xfac
     const dim3 grid((tiles + nw - 1) / nw), block(64 * nw);
     hipLaunchKernelGGL((k_qgemm_small<WB, MT, PERROW, SK, XK, YK>), grid, block, 0, s,
                        reinterpret_cast<const uint8_t*>(a.w), a.s, x, y, m, a.n_out, a.k,
-                       a.group_size, a.xor_mask, xfac, epi);
+                       a.group_size, a.xor_mask, xfac, a.wfold, epi);
 }
 
 template <int WB, bool PERROW, ScaleKind SK, XKind XK, YKind YK>
@@ -429,15 +449,28 @@ __global__ __launch_bounds__(256) void k_row_factors(const void* __restrict__ X,
     if (threadIdx.x == 0) fac[row] = row_pow2_factor(mx, XK == XKind::F32 ? 23 : 7);
 }
 
+// Workspace: [scale folds: n_out floats (int4), padded to 16 B] [activation factors: m floats].
+static size_t fold_bytes(const QArgs& a) {
+    return a.wbits == 4 ? (((size_t)a.n_out * sizeof(float) + 15) & ~(size_t)15) : 0;
+}
+
 size_t qgemm_small_workspace(const QArgs& a) {
-    return a.x_kind == XKind::F16 ? 0 : (size_t)a.m * sizeof(float);
+    return fold_bytes(a) + (a.x_kind == XKind::F16 ? 0 : (size_t)a.m * sizeof(float));
 }
 
 hipError_t launch_qgemm_small(const QArgs& a0, void* workspace, hipStream_t s) {
     QArgs a = a0;
     a.xfac = nullptr;
+    a.wfold = nullptr;
+    if (a.wbits == 4) {
+        float* fold = static_cast<float*>(workspace);
+        if (hipError_t e = launch_scale_fold(a.s, a.scale_kind, a.n_out, a.k / a.group_size, fold, s);
+            e != hipSuccess)
+            return e;
+        a.wfold = fold;
+    }
     if (a.x_kind == XKind::BF16 || a.x_kind == XKind::F32) {
-        float* fac = static_cast<float*>(workspace);
+        float* fac = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + fold_bytes(a));
         if (a.x_kind == XKind::BF16)
             hipLaunchKernelGGL(k_row_factors<XKind::BF16>, dim3(a.m), dim3(256), 0, s, a.x, a.k, fac);
         else
@@ -452,6 +485,29 @@ hipError_t launch_qgemm_small(const QArgs& a0, void* workspace, hipStream_t s) {
         ok = launch_s<4, false>(a, s);
     }
     if (!ok) return hipErrorInvalidValue;
+    return hipGetLastError();
+}
+
+// One wave per weight row: fold[n] = scale_fold_factor(max_g |s(n, g)|).
+template <ScaleKind SK>
+__global__ __launch_bounds__(256) void k_scale_fold(const void* __restrict__ S, int N, int G,
+                                                    float* __restrict__ fold) {
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= N) return;
+    const float f = row_scale_fold<SK>(S, (size_t)row, G, threadIdx.x & 63);
+    if ((threadIdx.x & 63) == 0) fold[row] = f;
+}
+
+hipError_t launch_scale_fold(const void* s, ScaleKind sk, int n_out, int groups, float* fold, hipStream_t st) {
+    const dim3 grid((n_out + 3) / 4), block(256);
+    switch (sk) {
+        case ScaleKind::F16: hipLaunchKernelGGL(k_scale_fold<ScaleKind::F16>, grid, block, 0, st, s, n_out, groups, fold); break;
+        case ScaleKind::F32: hipLaunchKernelGGL(k_scale_fold<ScaleKind::F32>, grid, block, 0, st, s, n_out, groups, fold); break;
+        case ScaleKind::GroupScale:
+            hipLaunchKernelGGL(k_scale_fold<ScaleKind::GroupScale>, grid, block, 0, st, s, n_out, groups, fold);
+            break;
+        default: return hipErrorInvalidValue;
+    }
     return hipGetLastError();
 }
 

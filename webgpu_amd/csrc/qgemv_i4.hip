@@ -303,7 +303,8 @@ bool qgemv_i4_fast(const QArgs& a) {
     const int spg = a.group_size / 32;
     return a.x_kind == XKind::F16 && a.k % 32 == 0 && a.k <= 16384 && a.group_size % 32 == 0 && spg > 0 &&
            (spg & (spg - 1)) == 0 && (a.scale_kind != ScaleKind::F16 || (a.k / a.group_size) % 2 == 0) &&
-           a.scale_kind != ScaleKind::None && ((uintptr_t)a.w & 15u) == 0 && ((uintptr_t)a.x & 15u) == 0;
+           a.scale_kind != ScaleKind::None && ((uintptr_t)a.w & 15u) == 0 && ((uintptr_t)a.x & 15u) == 0 &&
+           ((uintptr_t)a.s & 3u) == 0;  // fp16 scales are read as aligned u32 pairs
 }
 
 hipError_t launch_qgemv_i4(const QArgs& a, hipStream_t s) {

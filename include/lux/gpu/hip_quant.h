@@ -135,6 +135,27 @@ LuxBackendError lux_hip_qmatmul_ex(LuxBackendContext* ctx, const LuxHipQMatmulDe
                                    LuxBackendBuffer* bias, LuxBackendBuffer* residual,
                                    LuxBackendBuffer* y);
 
+/* No counterpart in the reference: for callers that cannot allocate device memory (code
+ * under HIP graph capture, serving loops that forbid hipMalloc).  Same arguments, checks
+ * and results as lux_hip_qmatmul_ex, but the staging buffers of the kernels (activations
+ * restaged as fp16 and their row factors, the weight rows' scale folds, per-token int8
+ * activations for QUANTIZE_X) live in a fixed per-device array of
+ * LUX_HIP_NOALLOC_SCRATCH_BYTES inside the library instead of the context workspace.
+ * No hipMalloc / hipFree or other allocating call is made (the first call on a device
+ * looks up that device's array).  A shape that needs more scratch than the maximum
+ * returns NOT_SUPPORTED: the large-m int4 GEMM needs m*k*2 + m*4 + n_out*4 bytes (config 4:
+ * 16.8 MB), QUANTIZE_X m*k + m*4, the small-m int4 GEMM n_out*4 (+ m*4 for bf16/f32 x).
+ * The array holds the last call's contents; every kernel writes what it reads there
+ * first, so nothing needs clearing.  All calls on one GPU share its array: calls that
+ * overlap in time on one GPU (any context, any stream) race and must be serialised by
+ * the caller. */
+#define LUX_HIP_NOALLOC_SCRATCH_BYTES (32u << 20)
+LuxBackendError lux_hip_qmatmul_noalloc(LuxBackendContext* ctx, const LuxHipQMatmulDesc* desc,
+                                        LuxBackendBuffer* w, LuxBackendBuffer* w_scales,
+                                        LuxBackendBuffer* x, LuxBackendBuffer* x_scales, int epilogue,
+                                        LuxBackendBuffer* bias, LuxBackendBuffer* residual,
+                                        LuxBackendBuffer* y);
+
 /* ---- producers and codecs of the matmul inputs ------------------------------ */
 
 /* Descriptor of one symmetric group quantization of X [rows x k] along k. */

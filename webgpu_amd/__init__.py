@@ -148,6 +148,8 @@ EXPORTS = {
                                 c_void_p, c_void_p]),
     "lux_hip_qmatmul_ex": (c_int, [c_void_p, POINTER(QMatmulDesc), c_void_p, c_void_p, c_void_p,
                                    c_void_p, c_int, c_void_p, c_void_p, c_void_p]),
+    "lux_hip_qmatmul_noalloc": (c_int, [c_void_p, POINTER(QMatmulDesc), c_void_p, c_void_p, c_void_p,
+                                        c_void_p, c_int, c_void_p, c_void_p, c_void_p]),
     "lux_hip_rms_norm": (c_int, [c_void_p, POINTER(RmsNormParams), c_void_p, c_void_p, c_void_p,
                                  c_void_p]),
     "lux_hip_quantize": (c_int, [c_void_p, POINTER(QuantizeDesc), c_void_p, c_void_p, c_void_p]),
@@ -402,6 +404,15 @@ class Context:
             self.handle, byref(desc), w.handle, scales.handle if scales else None, x.handle,
             x_scales.handle if x_scales else None, epilogue, bias.handle if bias else None,
             residual.handle if residual else None, y.handle), "qmatmul_ex")
+
+    def qmatmul_noalloc(self, desc: QMatmulDesc, w: Buffer, scales: Buffer | None, x: Buffer,
+                        x_scales: Buffer | None, epilogue: int, bias: Buffer | None,
+                        residual: Buffer | None, y: Buffer):
+        """lux_hip_qmatmul_ex with the library's fixed per-device scratch (no allocation)."""
+        self.plugin.check(self.lib.lux_hip_qmatmul_noalloc(
+            self.handle, byref(desc), w.handle, scales.handle if scales else None, x.handle,
+            x_scales.handle if x_scales else None, epilogue, bias.handle if bias else None,
+            residual.handle if residual else None, y.handle), "qmatmul_noalloc")
 
     def rms_norm(self, x: Buffer, gamma: Buffer, y: Buffer, rows: int, hidden: int,
                  eps: float = 1e-6, x_dtype: int = F32, y_dtype: int = F32,

@@ -20,6 +20,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <mutex>
 #include <string>
 #include <thread>
 #include <vector>
@@ -93,6 +94,38 @@ LuxBackendError get_workspace(HipCtx* c, size_t bytes, void** out, const char* o
     c->ws = p;
     c->ws_size = sz;
     *out = p;
+    return LUX_BACKEND_OK;
+}
+
+// ---- fixed scratch of lux_hip_qmatmul_noalloc -------------------------------------
+// One array per GPU, in the code object's device memory (allocated when the library's
+// code is loaded on that device, held until the process ends).  In host code `scratch`
+// names a host-side stand-in, not the device array: kernels and copies get the address
+// from scratch_device_ptr(), which asks HIP for it once per device.
+constexpr size_t kScratchBytes = LUX_HIP_NOALLOC_SCRATCH_BYTES;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// Device address of `scratch` on `device`, which must be the current device.
+LuxBackendError scratch_device_ptr(int device, void** out) {
+    *out = nullptr;
+    if (device < 0 || device >= kMaxDevices)
+        return fail(LUX_BACKEND_ERROR_NOT_SUPPORTED, "qmatmul_noalloc: device %d beyond %d", device, kMaxDevices);
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[device]) {
+        void* p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p) {
+            (void)hipGetLastError();
+            return fail(LUX_BACKEND_ERROR_INTERNAL, "qmatmul_noalloc: hipGetSymbolAddress(scratch) on device %d: %s",
+                        device, hipGetErrorString(e));
+        }
+        g_scratch_ptr[device] = p;
+    }
+    *out = g_scratch_ptr[device];
     return LUX_BACKEND_OK;
 }
 
@@ -559,10 +592,12 @@ LUX_EXPORT LuxBackendError lux_hip_gemv_f16(LuxBackendContext* ctx, LuxBackendBu
 }
 
 namespace {
+// noalloc: staging buffers come from the device's fixed `scratch` array (at most
+// kScratchBytes) instead of the context workspace; nothing is allocated.
 LuxBackendError qmatmul_impl(LuxBackendContext* ctx, const LuxHipQMatmulDesc* d, LuxBackendBuffer* w,
                              LuxBackendBuffer* w_scales, LuxBackendBuffer* x, LuxBackendBuffer* x_scales,
                              int epilogue, LuxBackendBuffer* bias, LuxBackendBuffer* residual,
-                             LuxBackendBuffer* y) {
+                             LuxBackendBuffer* y, bool noalloc = false) {
     HipCtx* c = C(ctx);
     if (!c || !d || !w || !x || !y) return fail(LUX_BACKEND_ERROR_INVALID_ARGUMENT, "qmatmul: NULL argument");
     if (epilogue < LUX_HIP_EPILOGUE_NONE || epilogue > LUX_HIP_EPILOGUE_SILU_MUL)
@@ -633,6 +668,14 @@ LuxBackendError qmatmul_impl(LuxBackendContext* ctx, const LuxHipQMatmulDesc* d,
 
     if (LuxBackendError e = begin_op(c, "qmatmul")) return e;
     if (M == 0 || n_out == 0) return LUX_BACKEND_OK;
+    auto workspace = [&](size_t bytes, void** out) -> LuxBackendError {
+        if (!noalloc) return get_workspace(c, bytes, out, "qmatmul");
+        if (bytes > kScratchBytes)
+            return fail(LUX_BACKEND_ERROR_NOT_SUPPORTED,
+                        "qmatmul_noalloc: this shape needs %zu bytes of scratch, above the maximum of %zu", bytes,
+                        kScratchBytes);
+        return scratch_device_ptr(c->device, out);
+    };
 
     QArgs a{};
     a.w = W->ptr;
@@ -661,7 +704,7 @@ LuxBackendError qmatmul_impl(LuxBackendContext* ctx, const LuxHipQMatmulDesc* d,
         if (qx) {  // int8 activations and their f32 per-token scales in the workspace
             a.x_kind = XKind::I8;
             void* wsv = nullptr;
-            if (LuxBackendError e = get_workspace(c, (size_t)M * K + (size_t)M * 4, &wsv, "qmatmul")) return e;
+            if (LuxBackendError e = workspace((size_t)M * K + (size_t)M * 4, &wsv)) return e;
             uint8_t* ws = static_cast<uint8_t*>(wsv);
             a.x = ws;
             a.xs = reinterpret_cast<const float*>(ws + (size_t)M * K);
@@ -691,17 +734,17 @@ LuxBackendError qmatmul_impl(LuxBackendContext* ctx, const LuxHipQMatmulDesc* d,
         const size_t wsb = qgemm_small_workspace(a);
         void* ws = nullptr;
         if (wsb)
-            if (LuxBackendError e = get_workspace(c, wsb, &ws, "qmatmul")) return e;
+            if (LuxBackendError e = workspace(wsb, &ws)) return e;
         he = launch_qgemm_small(a, ws, c->stream);
     } else if (d->weight_bits == 4 && qgemm_i4_large_supported(a)) {
         void* ws = nullptr;
-        if (LuxBackendError e = get_workspace(c, qgemm_i4_large_workspace(a), &ws, "qmatmul")) return e;
+        if (LuxBackendError e = workspace(qgemm_i4_large_workspace(a), &ws)) return e;
         he = launch_qgemm_i4_large(a, ws, c->stream);
     } else if (qgemm_small_supported(a)) {
         const size_t wsb = qgemm_small_workspace(a);
         void* ws = nullptr;
         if (wsb)
-            if (LuxBackendError e = get_workspace(c, wsb, &ws, "qmatmul")) return e;
+            if (LuxBackendError e = workspace(wsb, &ws)) return e;
         he = launch_qgemm_small(a, ws, c->stream);
     } else {
         return fail(LUX_BACKEND_ERROR_NOT_SUPPORTED, "qmatmul: no kernel for this descriptor");
@@ -723,6 +766,14 @@ LUX_EXPORT LuxBackendError lux_hip_qmatmul_ex(LuxBackendContext* ctx, const LuxH
                                               LuxBackendBuffer* bias, LuxBackendBuffer* residual,
                                               LuxBackendBuffer* y) {
     return qmatmul_impl(ctx, d, w, w_scales, x, x_scales, epilogue, bias, residual, y);
+}
+
+LUX_EXPORT LuxBackendError lux_hip_qmatmul_noalloc(LuxBackendContext* ctx, const LuxHipQMatmulDesc* d,
+                                                   LuxBackendBuffer* w, LuxBackendBuffer* w_scales,
+                                                   LuxBackendBuffer* x, LuxBackendBuffer* x_scales, int epilogue,
+                                                   LuxBackendBuffer* bias, LuxBackendBuffer* residual,
+                                                   LuxBackendBuffer* y) {
+    return qmatmul_impl(ctx, d, w, w_scales, x, x_scales, epilogue, bias, residual, y, true);
 }
 
 // ---------------------------------------------------------------- producers / codecs

@@ -70,3 +70,17 @@ def test_no_device_behaviour():
         pytest.skip("a HIP device is visible")
     assert p.vt_create(0) is None
     assert "device" in p.last_error()
+
+
+def test_c_loader_compiles_as_c11():
+    """The headers serve a plain C caller: tests/c_loader builds with gcc -std=c11 -pedantic
+    -Werror against include/ alone (no HIP headers), and links only libdl."""
+    here = os.path.join(os.path.dirname(os.path.abspath(__file__)), "c_loader")
+    subprocess.run(["make", "-B", "-C", here], check=True, capture_output=True)
+    exe = os.path.join(here, "lux_loader_check")
+    assert os.access(exe, os.X_OK)
+    out = subprocess.run(["nm", "-D", "--undefined-only", exe], capture_output=True, text=True,
+                         check=True).stdout
+    assert "hip" not in out.lower()
+    usage = subprocess.run([exe], capture_output=True, text=True)
+    assert usage.returncode == 2 and "usage" in usage.stderr

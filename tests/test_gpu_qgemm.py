@@ -258,3 +258,38 @@ def test_int4_small_m_formats(ctx, fmt, coding):
     got = _run(ctx, d, Wp, sbuf, X, n_out, m, "f16")
     ref = oracle.matmul_nax_grouped_tokens(Wp, sref.reshape(-1), Xf, gs, coding)
     compare(got, round_to(ref, "f16"), f"small-m formats {fmt} {coding}")
+
+
+@pytest.mark.parametrize("n_out,K,m,sf,y", [
+    (1000, 2048, 1, "f16", "f16"),      # rows not a multiple of 16, one token
+    (4099, 4096, 5, "f32", "f32"),
+    (333, 2048, 16, "gs", "bf16"),      # GroupScale records, a full m-tile
+    (777, 2048, 17, "none", "f32"),     # no scales, two m-tiles with one token in the second
+    (1024, 6144, 32, "f16", "f16"),     # three 1024-k super-chunks per call
+    (2051, 3072, 9, "f16", "f16"),      # k not a multiple of 2048 at m <= 16: the general kernel
+])
+def test_int8_per_row_fp16_x(ctx, n_out, K, m, sf, y):
+    """int8 weights with one scale per row and fp16 activations, m <= 32: the kernel that
+    stages X in super-chunks and decodes int8 with SDWA conversions, against the oracle
+    (dequantize_nax_int8_group with gs = K, then the sequential-k matmul)."""
+    r = rng(n_out + K + 11 * m)
+    q, s16 = int8_weights(r, n_out, K)
+    s32 = s16.astype(np.float32).reshape(-1)
+    if sf == "f16":
+        s, code = s16, W.SCALE_F16
+    elif sf == "f32":
+        s32 = r.uniform(1e-3, 1e-2, size=n_out).astype(np.float32)
+        s, code = s32, W.SCALE_F32
+    elif sf == "gs":
+        s32 = r.uniform(1e-3, 1e-2, size=n_out).astype(np.float32)
+        s = np.zeros((n_out, 4), np.float32)
+        s[:, 0] = s32
+        code = W.SCALE_GROUPSCALE
+    else:
+        s32 = np.ones(n_out, np.float32)
+        s, code = np.zeros(4, np.float32), W.SCALE_NONE
+    X, Xf, xc = _x(r, m, K, "f16")
+    d = W.qdesc(n_out, K, m, 8, K, 0, code, xc, YD[y][0])
+    got = _run(ctx, d, q, s, X, n_out, m, y)
+    ref = oracle.matmul_int8_dequant_tokens(q, s32, Xf, K)
+    compare(got, round_to(ref, y), f"int8 per-row {n_out}x{K} m{m} {sf}")

@@ -240,6 +240,20 @@ __device__ __forceinline__ float wave_sum(float v) {
 // Launchers (host side).  Plain pointers and sizes; shapes are validated by the
 // caller in plugin.hip before any launch, so every grid below stays in bounds.
 // ---------------------------------------------------------------------------
+// Compute units of the current device, cached per device (host code).
+inline int device_cus() {
+    static int cus[64] = {0};
+    int dev = 0;
+    (void)hipGetDevice(&dev);
+    if (dev < 0 || dev >= 64) return 256;
+    if (!cus[dev]) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+        cus[dev] = n;
+    }
+    return cus[dev];
+}
+
 struct QArgs {
     const void* w;        // packed weights
     const void* s;        // weight scales (may be null for ScaleKind::None)

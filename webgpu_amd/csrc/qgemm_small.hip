@@ -338,6 +338,252 @@ __global__ __launch_bounds__(64 * MAXW) void k_qgemm_small(
     }
 }
 
+// ---------------------------------------------------------------- int8, per-row scales, fp16 X
+// The config-3 shape (int8 weights, one scale per row, fp16 activations, m <= 32) as a
+// streaming kernel: HBM delivers contiguous spans far better than the 16 rows x 64 bytes
+// per instruction that loading the MFMA layout straight into registers takes (on a
+// 235 MB stream with 7 waves per CU: 7.1 against 5.4 TB/s), so
+//   - each wave streams its 16 weight rows into its own LDS ring with direct-to-LDS loads,
+//     4 rows x 256 contiguous bytes per instruction (one 256-k chunk of 16 rows = 4 loads),
+//     R_PD chunks ahead; 16-byte unit b of tile row r sits at unit b ^ r of the row, so the
+//     fragment reads (16 rows of one unit) hit 16 distinct bank groups;
+//   - X goes global -> LDS the same way in super-chunks of R_SKC k (all rows of the
+//     m-tiles, double-buffered): the block meets at a barrier once per super-chunk;
+//   - int8 -> fp16 is exact and in natural k order: v_cvt_f16_i16 with SDWA reads a
+//     sign-extended byte and writes one half of the register, 4 VALU per 4 weights.
+//   - Lane (row r16, quarter kq) feeds k = 64 l + 16 kq + 8 st + 0..7 of a chunk to k-step
+//     (l, st); the X fragment of token t is the same 16 bytes of X row t.
+// A wave waits only for its own loads (s_waitcnt); the barrier publishes X.
+namespace {
+constexpr int R_PD = 3;      // weight chunks (256 k) in flight per wave
+constexpr int R_XJ = 8;      // X loads per wave per super-chunk (<= 32 jobs, >= 4 waves)
+// k per X super-chunk: 1024 with one m-tile, 512 with two (the double-buffered X then fits
+// beside 7 weight rings)
+constexpr int r_skc(int mt) { return mt == 1 ? 1024 : 512; }
+constexpr int r_xp(int mt) { return 2 * r_skc(mt) + 16; }  // bytes per staged X row (+16: conflict-free)
+
+// Two signed bytes of w (BYTE_0/1 or BYTE_2/3) -> two fp16, exact.
+__device__ __forceinline__ uint32_t i8pair_lo_f16(uint32_t w) {
+    uint32_t r;
+    asm("v_cvt_f16_i16_sdwa %0, sext(%1) dst_sel:WORD_0 dst_unused:UNUSED_PAD src0_sel:BYTE_0\n\t"
+        "v_cvt_f16_i16_sdwa %0, sext(%1) dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:BYTE_1"
+        : "=&v"(r)
+        : "v"(w));
+    return r;
+}
+__device__ __forceinline__ uint32_t i8pair_hi_f16(uint32_t w) {
+    uint32_t r;
+    asm("v_cvt_f16_i16_sdwa %0, sext(%1) dst_sel:WORD_0 dst_unused:UNUSED_PAD src0_sel:BYTE_2\n\t"
+        "v_cvt_f16_i16_sdwa %0, sext(%1) dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:BYTE_3"
+        : "=&v"(r)
+        : "v"(w));
+    return r;
+}
+
+// s_waitcnt vmcnt(n) with lgkmcnt(0) (expcnt at its maximum), and vmcnt(n) alone.
+constexpr int r_vmcnt_lgkm0(int n) { return (n & 0xF) | ((n >> 4) << 14) | (0x7 << 4); }
+constexpr int r_vmcnt(int n) { return (n & 0xF) | ((n >> 4) << 14) | (0x7 << 4) | (0xF << 8); }
+
+template <int N>
+__device__ __forceinline__ void wait_vm() { __builtin_amdgcn_s_waitcnt(r_vmcnt(N)); }
+
+size_t i8row_lds(int mt, int nw) { return (size_t)2 * 16 * mt * r_xp(mt) + (size_t)nw * R_PD * 4096 + 1024; }
+}  // namespace
+
+template <int MT, ScaleKind SK, YKind YK>
+__global__ __launch_bounds__(64 * MAXW) void k_qgemm_i8row(const uint8_t* __restrict__ W, const void* __restrict__ S,
+                                                         const f16* __restrict__ X, void* __restrict__ Y, int M, int N,
+                                                         int K, EpiArgs epi) {
+    // LDS: X [2][16 MT][R_XP] | weight rings [nw][R_PD][16 rows x 256 B] | spare 1 KB
+    extern __shared__ __attribute__((aligned(16))) uint8_t xl[];
+    const int nw = blockDim.x >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int n0 = (blockIdx.x * nw + wv) * 16;
+    const int r16 = lane & 15, kq = lane >> 4;
+    constexpr int R_SKC = r_skc(MT), R_XP = r_xp(MT), CPS = R_SKC / 256;
+    constexpr int XB = 16 * MT * R_XP;  // bytes per X buffer
+    uint8_t* ring = xl + 2 * XB + wv * (R_PD * 4096);
+    uint8_t* spare = xl + 2 * XB + nw * (R_PD * 4096);
+    const int nchunks = K / 256, nsc = K / R_SKC;
+
+    // X super-chunk loads: job j = 1 KB segment j % SEGS of token row j / SEGS (at most 32
+    // jobs); wave w takes j = w + nw i.  Every wave issues R_XJ of them (the ones past the
+    // last job read zeros into the spare 1 KB), so the count between any two loads of a wave
+    // is fixed.
+    const __amdgpu_buffer_rsrc_t rx =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<f16*>(X), (short)0, (int)((size_t)M * K * 2), 0x00020000);
+    constexpr int SEGS = R_SKC / 512;  // 1 KB segments per X row and super-chunk
+    auto load_x = [&](int sc) {
+        uint8_t* buf = xl + (sc & 1) * XB;
+        const int k0 = min(sc, nsc - 1) * R_SKC;  // past the end: re-read the last (never used)
+#pragma unroll
+        for (int i = 0; i < R_XJ; ++i) {
+            const int j = wv + nw * i;  // job: row j / SEGS, segment j % SEGS
+            const bool ok = j < M * SEGS;
+            const int row = j / SEGS, sg = j % SEGS;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                rx, (__attribute__((address_space(3))) void*)(ok ? buf + row * R_XP + 1024 * sg : spare), 16,
+                ok ? (row * K + k0 + 512 * sg) * 2 + 16 * lane : M * K * 2, 0, 0, 0);
+        }
+    };
+
+    // Weight loads of chunk c: instruction j covers tile rows 4 j .. 4 j + 3, 256 bytes each;
+    // lane l -> row r = 4 j + l / 16, unit p = l % 16 of its LDS row, global unit p ^ r.
+    // Rows past N re-read row N - 1 (never stored).
+    const __amdgpu_buffer_rsrc_t rw =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(W), (short)0, (int)((size_t)N * K), 0x00020000);
+    int woff[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int r = 4 * j + (lane >> 4), p = lane & 15;
+        woff[j] = min(n0 + r, N - 1) * K + 16 * (p ^ r);
+    }
+    auto load_w = [&](int c) {
+        const int cc = min(c, nchunks - 1);  // past the end: re-read the last chunk (never used)
+        uint8_t* slot = ring + (c % R_PD) * 4096;
+        const int so = __builtin_amdgcn_readfirstlane(cc * 256);
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (__attribute__((address_space(3))) void*)(slot + 1024 * j), 16,
+                                                     woff[j], so, 0, 0);
+    };
+
+    f32x4 acc[MT];
+#pragma unroll
+    for (int t = 0; t < MT; ++t) acc[t] = f32x4{};
+
+    load_x(0);
+#pragma unroll
+    for (int i = 0; i < R_PD; ++i) load_w(i);
+
+    // Issue order per super-chunk: chunk p = 0 refills W(c + R_PD) then X(sc + 1); chunks
+    // 1 .. CPS-1 refill W(c + R_PD).  The prologue (X(0), W(0..2)) has the same shape, so
+    // the counts below hold from the start:
+    //   - at the barrier, X(sc) is complete once the weight loads issued after it may
+    //     remain: CPS == 4: W(c+1 .. c+3) = 12 loads; CPS == 2: W(c+2) = 4 (the barrier then
+    //     also completes W(c), W(c+1));
+    //   - chunk c's weights: the loads issued after W(c) (4 per chunk, R_XJ for an X
+    //     super-chunk): CPS == 4: 8 at p = 0 and 16 at p = 1..3; CPS == 2: covered by the
+    //     barrier at p = 0, 24 at p = 1.
+    constexpr int WB_BAR = CPS == 4 ? 12 : 4;
+    const int wrd = r16 * 256;  // this lane's row in a ring slot
+    for (int sc = 0; sc < nsc; ++sc) {
+        // the barrier publishes every wave's share of X(sc) and retires the other X buffer
+        // (read in super-chunk sc - 1) for X(sc + 1)
+        __builtin_amdgcn_s_waitcnt(r_vmcnt_lgkm0(WB_BAR));
+        asm volatile("s_barrier" ::: "memory");
+        const uint8_t* xbuf = xl + (sc & 1) * XB;
+#pragma unroll
+        for (int p = 0; p < CPS; ++p) {
+            const int c = CPS * sc + p;
+            if (CPS == 4) {
+                if (p == 0) wait_vm<8>();
+                else wait_vm<16>();
+            } else {
+                if (p == 0) wait_vm<WB_BAR>();
+                else wait_vm<24>();
+            }
+            const uint8_t* slot = ring + (c % R_PD) * 4096 + wrd;
+            u32x4 q[4];
+#pragma unroll
+            for (int l = 0; l < 4; ++l) q[l] = *reinterpret_cast<const u32x4*>(slot + 16 * ((4 * l + kq) ^ r16));
+            __builtin_amdgcn_s_waitcnt(r_vmcnt_lgkm0(63));  // the slot is read: refill it
+            load_w(c + R_PD);
+            if (p == 0) load_x(sc + 1);
+            f16x8 av[4][2];
+#pragma unroll
+            for (int l = 0; l < 4; ++l) {
+                av[l][0] = __builtin_bit_cast(f16x8, u32x4{i8pair_lo_f16(q[l].x), i8pair_hi_f16(q[l].x),
+                                                           i8pair_lo_f16(q[l].y), i8pair_hi_f16(q[l].y)});
+                av[l][1] = __builtin_bit_cast(f16x8, u32x4{i8pair_lo_f16(q[l].z), i8pair_hi_f16(q[l].z),
+                                                           i8pair_lo_f16(q[l].w), i8pair_hi_f16(q[l].w)});
+            }
+            const uint8_t* xb = xbuf + p * 512;
+#pragma unroll
+            for (int l = 0; l < 4; ++l)
+#pragma unroll
+                for (int st = 0; st < 2; ++st)
+#pragma unroll
+                    for (int t = 0; t < MT; ++t) {
+                        const f16x8 bx =
+                            *reinterpret_cast<const f16x8*>(xb + (16 * t + r16) * R_XP + 2 * (64 * l + 16 * kq + 8 * st));
+                        acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[l][st], bx, acc[t], 0, 0, 0);
+                    }
+        }
+    }
+    __builtin_amdgcn_s_waitcnt(r_vmcnt_lgkm0(0));  // no LDS load may land after the block ends
+
+    // epilogue: D[i][j] of a 16x16 tile sits in lane j + 16 (i / 4), register i % 4;
+    // i = weight row (n), j = token (m).
+#pragma unroll
+    for (int t = 0; t < MT; ++t) {
+        const int m = 16 * t + r16;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int n = n0 + 4 * kq + r;
+            if (m < M && n < N) {
+                const float v = acc[t][r] * load_scale_t<SK>(S, (size_t)n);
+                store_y<YK>(Y, (size_t)m * N + n, apply_epi(v, epi, m, n, N));
+            }
+        }
+    }
+}
+
+// The fast path above: int8, one scale per row (or none), fp16 X, m <= 32, no gated pair,
+// K a multiple of the super-chunk, byte offsets within 31 bits.
+static bool i8row_ok(const QArgs& a) {
+    const bool perrow = a.group_size == a.k || a.scale_kind == ScaleKind::None;
+    return a.wbits == 8 && perrow && a.x_kind == XKind::F16 && a.m <= 32 && a.epi.kind != (int)Epi::SiluMul &&
+           a.k % r_skc(a.m <= 16 ? 1 : 2) == 0 && (size_t)a.m * a.k * 2 < (1ull << 31) && (size_t)a.n_out * a.k < (1ull << 31) &&
+           ((uintptr_t)a.x & 15u) == 0 && ((uintptr_t)a.w & 15u) == 0;
+}
+
+template <int MT, ScaleKind SK, YKind YK>
+static void launch_i8row(const QArgs& a, hipStream_t s) {
+    const int cus = device_cus();
+    const int tiles = (a.n_out + 15) / 16;
+    int nw = 4;
+    if (tiles % cus == 0 && tiles / cus <= MAXW) nw = tiles / cus;
+    else if (tiles <= cus * MAXW && tiles >= cus) nw = (tiles + cus - 1) / cus;
+    nw = std::max(4, std::min(nw, MAXW));  // >= 4: the X loads of a super-chunk fit R_XJ per wave
+    while (i8row_lds(MT, nw) > 160 * 1024) --nw;
+    static bool attr = [] {
+        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&k_qgemm_i8row<MT, SK, YK>),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+        return true;
+    }();
+    (void)attr;
+    hipLaunchKernelGGL((k_qgemm_i8row<MT, SK, YK>), dim3((tiles + nw - 1) / nw), dim3(64 * nw), i8row_lds(MT, nw), s,
+                       reinterpret_cast<const uint8_t*>(a.w), a.s, reinterpret_cast<const f16*>(a.x), a.y, a.m,
+                       a.n_out, a.k, a.epi);
+}
+
+template <ScaleKind SK, YKind YK>
+static void launch_i8row_m(const QArgs& a, hipStream_t s) {
+    if (a.m <= 16) launch_i8row<1, SK, YK>(a, s);
+    else launch_i8row<2, SK, YK>(a, s);
+}
+
+template <ScaleKind SK>
+static bool launch_i8row_y(const QArgs& a, hipStream_t s) {
+    switch (a.y_kind) {
+        case YKind::F32: launch_i8row_m<SK, YKind::F32>(a, s); return true;
+        case YKind::F16: launch_i8row_m<SK, YKind::F16>(a, s); return true;
+        case YKind::BF16: launch_i8row_m<SK, YKind::BF16>(a, s); return true;
+        default: return false;
+    }
+}
+
+static bool launch_i8row_any(const QArgs& a, hipStream_t s) {
+    switch (a.scale_kind) {
+        case ScaleKind::F16: return launch_i8row_y<ScaleKind::F16>(a, s);
+        case ScaleKind::F32: return launch_i8row_y<ScaleKind::F32>(a, s);
+        case ScaleKind::GroupScale: return launch_i8row_y<ScaleKind::GroupScale>(a, s);
+        case ScaleKind::None: return launch_i8row_y<ScaleKind::None>(a, s);
+        default: return false;
+    }
+}
+
 bool qgemm_small_supported(const QArgs& a) {
     if (a.x_kind == XKind::I8 || a.y_kind == YKind::I32) return false;
     // weights and activations are read with 16-byte vector loads
@@ -478,7 +724,9 @@ hipError_t launch_qgemm_small(const QArgs& a0, void* workspace, hipStream_t s) {
         a.xfac = fac;
     }
     bool ok;
-    if (a.wbits == 8) {
+    if (i8row_ok(a)) {
+        ok = launch_i8row_any(a, s);
+    } else if (a.wbits == 8) {
         const bool perrow = a.group_size == a.k || a.scale_kind == ScaleKind::None;
         ok = perrow ? launch_s<8, true>(a, s) : launch_s<8, false>(a, s);
     } else {

@@ -189,19 +189,6 @@ __global__ __launch_bounds__(256) void k_qgemv_i4_generic(const uint32_t* __rest
     if (lane == 0) store_y<YK>(y, row, apply_epi(acc, epi, 0, row, n_out));
 }
 
-static int device_cus() {
-    static int cus[64] = {0};
-    int dev = 0;
-    (void)hipGetDevice(&dev);
-    if (dev < 0 || dev >= 64) return 256;
-    if (!cus[dev]) {
-        int n = 0;
-        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
-        cus[dev] = n;
-    }
-    return cus[dev];
-}
-
 template <int SPL, int RW, int D, ScaleKind SK, YKind YK>
 static void launch_rwd(const QArgs& a, hipStream_t s) {
     const int waves = (a.n_out + RW - 1) / RW;

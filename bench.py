@@ -378,6 +378,30 @@ def bench_gemv_t(torch, W, ctx, steps, warmup):
                          "traffic": measured_traffic("gemvt")}}
 
 
+MFMA_F32_PEAK_TFLOPS = 157.3
+
+
+def bench_gemm_f32(torch, W, ctx, n, steps, warmup):
+    """op_matmul_f32 as a general GEMM, C[n x n] = A[n x n] B[n x n] fp32 (the vtable's
+    only matmul slot, src/webgpu_plugin.cpp:1721-1771; the reference README quotes 1024^2)."""
+    r = np.random.default_rng(50 + n)
+    A = r.standard_normal((n, n)).astype(np.float32)
+    B = r.standard_normal((n, n)).astype(np.float32)
+    ab, bb, cb = ctx.upload(A), ctx.upload(B), ctx.alloc(n * n * 4)
+
+    def launch(i):
+        ctx.matmul_f32(ab, bb, cb, n, n, n)
+
+    k = max(3, min(steps, 50))
+    per = timed_graph(torch, ctx, launch, k, max(1, warmup // 4)) / k
+    for b in (ab, bb, cb):
+        b.free()
+    tf = 2.0 * n * n * n / per / 1e12
+    return {"n": n, "us_per_launch": round(per * 1e6, 2), "value": round(tf, 2), "unit": "TFLOP/s",
+            "roofline": {"bound": "mfma", "achieved": round(tf, 2), "peak": MFMA_F32_PEAK_TFLOPS,
+                         "unit": "TFLOP/s", "frac": round(tf / MFMA_F32_PEAK_TFLOPS, 4), "traffic": None}}
+
+
 GH_BYTES = 14336 * 4096 * 2 + 4096 * 2 + 14336 * 4  # A (f16) + x read, y (f32) written
 
 
@@ -557,7 +581,7 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=10.0)
     ap.add_argument("--only", choices=["c1", "c2", "c3", "c4", "c5", "copy", "quant", "dequant", "gemvb",
-                                       "gemvt", "gemvh", "w8a8", "ffn"],
+                                       "gemvt", "gemvh", "w8a8", "ffn", "gemm"],
                     default=None,
                     help="run one leg only and log its timing (profiling); the JSON line comes "
                          "from the full run")
@@ -630,6 +654,11 @@ def main():
         gb = bench_gemv_batched(torch, W, ctx, args.steps, args.warmup)
         log(f"  gemv_batched {gb['us_per_launch']} us/launch, {gb['value']} GB/s")
         return
+    if args.only == "gemm":
+        for n in (1024, 4096):
+            gm = bench_gemm_f32(torch, W, ctx, n, args.steps, args.warmup)
+            log(f"  gemm_f32 {n}^3 {gm['us_per_launch']} us/launch, {gm['value']} TFLOP/s")
+        return
     log("bench: config 2 int4 GEMV")
     c2 = bench_c2(torch, W, ctx, args.steps, args.warmup)
     log(f"  C2 {c2['per_launch_s']*1e6:.2f} us/launch, {c2['gbs']:.1f} GB/s")
@@ -643,6 +672,7 @@ def main():
     except W.LuxError as e:
         log(f"  C4 skipped: {e}")
     c1, c3s, c5, c5f, qz, dq, gb, gt, gh, w8, ff = None, [], None, None, None, None, None, None, None, None, None
+    gms = []
     try:
         log("bench: config 1 fp32 GEMV through op_matmul_f32")
         c1 = bench_c1(torch, W, ctx, args.steps, args.warmup)
@@ -678,6 +708,10 @@ def main():
         log("bench: decode FFN step (rms_norm, gate/up + SILU_MUL, down + residual)")
         ff = bench_ffn(torch, W, ctx, args.steps, args.warmup)
         log(f"  decode FFN step {ff['us_per_step']} us/step, {ff['value']} GB/s")
+        log("bench: fp32 GEMM through op_matmul_f32, 1024^3 and 4096^3")
+        for n in (1024, 4096):
+            gms.append(bench_gemm_f32(torch, W, ctx, n, args.steps, args.warmup))
+            log(f"  gemm_f32 {n}^3 {gms[-1]['us_per_launch']} us/launch, {gms[-1]['value']} TFLOP/s")
     except W.LuxError as e:
         log(f"  C1/C3/C5 skipped: {e}")
     cpu, cpu4 = None, None
@@ -731,6 +765,7 @@ def main():
         "gemv_f32_transpose": gt,
         "gemv_f16": gh,
         "decode_ffn_step": ff,
+        "gemm_f32_op_matmul": gms or None,
     }
     print(json.dumps(out), flush=True)
     ctx.close()

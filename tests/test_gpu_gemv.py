@@ -237,3 +237,17 @@ def test_gemv_f32_transpose_inf_and_empty(ctx):
     yb2 = ctx.upload(y0)
     ctx.gemv_f32(a, xb, yb2, 0, N, 1.0, 3.0, trans=True)
     assert np.all(ctx.download(yb2, np.float32, N) == 6.0)
+
+
+@pytest.mark.parametrize("M,K,N", [(1024, 1024, 1024), (129, 260, 68), (2, 4, 4), (300, 1000, 516),
+                                   (1000, 36, 2000)])
+def test_matmul_f32_mfma(ctx, M, K, N):
+    """op_matmul_f32 on the fp32 matrix cores (rows 16-byte aligned: K, N multiples of 4),
+    both tile sizes and ragged edges, against the oracle's sequential-k matmul."""
+    r = rng(M * 3 + K + N)
+    A = r.standard_normal((M, K)).astype(np.float32)
+    B = r.standard_normal((K, N)).astype(np.float32)
+    ref = oracle.matmul_f32(A, B)
+    a, b, c = ctx.upload(A), ctx.upload(B), ctx.alloc(M * N * 4)
+    ctx.matmul_f32(a, b, c, M, K, N)
+    compare(ctx.download(c, np.float32, (M, N)), ref, f"matmul mfma {M}x{K}x{N}", rel_tol=1e-5)

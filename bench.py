@@ -625,6 +625,8 @@ def main():
     if args.only == "c5":
         c5 = bench_c5(torch, W, ctx, args.steps, args.warmup)
         log(f"  C5 {c5['us_per_launch']} us/launch, {c5['value']} TOP/s, {c5['hbm_gbs']} GB/s")
+        c5f = bench_c5_fp(torch, W, ctx, args.steps, args.warmup)
+        log(f"  C5 from fp32 activations {c5f['us_per_launch']} us/launch, {c5f['value']} TOP/s")
         return
     if args.only == "quant":
         qz = bench_quantize(torch, W, ctx, args.steps, args.warmup)

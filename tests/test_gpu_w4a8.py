@@ -149,6 +149,45 @@ def test_w4a8_quantize_x(ctx, xdt):
                     wb, sb, ctx.upload(xin), ctx.upload(ascale), y1)
 
 
+@pytest.mark.parametrize("n_out,K,m,gs,xdt,y", [
+    (11008, 4096, 256, 128, "f32", "f16"),  # config 5
+    (64, 4096, 1000, 128, "f16", "f32"),    # many token blocks, fp16 activations
+    (300, 8192, 70, 256, "bf16", "bf16"),   # long rows, ragged rows and tokens
+    (130, 128, 5, 128, "f32", "f32"),       # one stage
+    (1024, 2048, 64, 2048, "f32", "f16"),   # per-output-channel weight scales
+])
+def test_w4a8_quantize_x_shapes(ctx, n_out, K, m, gs, xdt, y):
+    """QUANTIZE_X over shapes and activation dtypes is bit-identical to the host-quantized
+    int8 path (quantize_rows_int8 = compute_group_scales NAX_INT8_SYM +
+    quantize_nax_int8_group with gs = K, quantized_nax.wgsl:204-212, 336-362).  Two calls
+    in a row, the second with other data and fewer tokens (the workspace is reused)."""
+    from util import bf16_bits
+    r = rng(n_out + K + m)
+    _, Wp, s = int4_weights(r, n_out, K, gs, 1)[0:3]
+    xcode = {"f32": W.F32, "f16": W.F16, "bf16": W.BF16}[xdt]
+    ycode, ynp = {"f16": (W.F16, np.float16), "f32": (W.F32, np.float32), "bf16": (W.BF16, np.uint16)}[y]
+    ybytes = 4 if y == "f32" else 2
+    wb, sb = ctx.upload(Wp), ctx.upload(s)
+    for rows, seed in ((m, 1), (max(1, m // 2 - 3), 2)):
+        x = rng(seed).standard_normal((rows, K)).astype(np.float32) * 3.0
+        if xdt == "bf16":
+            xin = bf16_bits(x)
+            xf = bf16_to_f32(xin)
+        elif xdt == "f16":
+            xin = x.astype(np.float16)
+            xf = xin.astype(np.float32)
+        else:
+            xin = xf = x
+        a8, ascale = quantize_rows_int8(xf)
+        y1, y2 = ctx.alloc(rows * n_out * ybytes), ctx.alloc(rows * n_out * ybytes)
+        ctx.qmatmul(W.qdesc(n_out, K, rows, 4, gs, 1, W.SCALE_F16, xcode, ycode, W.QFLAG_QUANTIZE_X),
+                    wb, sb, ctx.upload(xin), None, y1)
+        ctx.qmatmul(W.qdesc(n_out, K, rows, 4, gs, 1, W.SCALE_F16, W.I8, ycode), wb, sb, ctx.upload(a8),
+                    ctx.upload(ascale), y2)
+        got = ctx.download(y1, ynp, (rows, n_out)).view(np.uint8)
+        assert np.array_equal(got, ctx.download(y2, ynp, (rows, n_out)).view(np.uint8)), f"rows {rows}"
+
+
 # --------------------------------------------------------------------------- W8A8
 @pytest.mark.parametrize("n_out,K,m", [(512, 4096, 256), (97, 512, 300), (40, 256, 3)])
 def test_w8a8_full_k_int32_exact(ctx, n_out, K, m):

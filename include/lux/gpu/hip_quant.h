@@ -30,7 +30,7 @@
 extern "C" {
 #endif
 
-#define LUX_HIP_QUANT_API_VERSION 3u
+#define LUX_HIP_QUANT_API_VERSION 4u
 
 /* Element types.  The first four keep LuxDtype's numbering (docs/api.md:188-197). */
 typedef enum LuxHipDtype {
@@ -208,6 +208,34 @@ LuxBackendError lux_hip_convert_nibbles(LuxBackendContext* ctx, LuxBackendBuffer
  * GROUPSCALE written from F16/F32 carries zero_point 0 and group_min = group_max = 0. */
 LuxBackendError lux_hip_convert_scales(LuxBackendContext* ctx, LuxBackendBuffer* in, int in_format,
                                        LuxBackendBuffer* out, int out_format, size_t count);
+
+/* PerChannelScale (quantized.wgsl:51-56), one per channel_stride elements. */
+typedef struct LuxHipPerChannelScale {
+    float scale;
+    int32_t zero_point;
+    uint32_t _pad0;
+    uint32_t _pad1;
+} LuxHipPerChannelScale;
+
+/* quantize_int8_per_channel (quantized.wgsl:264-280) over `size` f32 elements of `in`
+ * into one i32 per element of `out`: the element's channel is index / channel_stride
+ * (ChannelQuantParams.channel_stride, :44-49) and channel_scales holds
+ * ceil(size / channel_stride) LuxHipPerChannelScale.  quant_type is QuantParams.quant_type
+ * (:37-42): 0 = quantize_int8_symmetric (:83-86), q = clamp(i32(round(x / s)), -128, 127);
+ * any other value = quantize_int8_asymmetric (:92-95), q = clamp(i32(round(x / s) +
+ * f32(zero_point)), -128, 127).  round() is half-to-even, x / s the IEEE quotient, i32()
+ * saturating (NaN -> 0).  Buffers 4-byte aligned. */
+LuxBackendError lux_hip_quantize_int8_per_channel(LuxBackendContext* ctx, LuxBackendBuffer* in,
+                                                  LuxBackendBuffer* channel_scales, LuxBackendBuffer* out,
+                                                  size_t size, uint32_t channel_stride, uint32_t quant_type);
+
+/* dequantize_int8_per_channel (quantized.wgsl:282-297): i32 per element in, f32 out;
+ * quant_type 0 = dequantize_int8_symmetric (:88-90), f32(q) * s; otherwise
+ * dequantize_int8_asymmetric (:97-99), f32(q - zero_point) * s with the i32 subtraction
+ * wrapping.  Channels and alignment as lux_hip_quantize_int8_per_channel. */
+LuxBackendError lux_hip_dequantize_int8_per_channel(LuxBackendContext* ctx, LuxBackendBuffer* in,
+                                                    LuxBackendBuffer* channel_scales, LuxBackendBuffer* out,
+                                                    size_t size, uint32_t channel_stride, uint32_t quant_type);
 
 /* requantize_int32_to_int8 (quantized.wgsl:560-580, RequantParams {size, input_scale,
  * output_scale, output_zero_point}): out[i] = clamp(i32(round(f32(in[i]) * input_scale /

@@ -58,6 +58,8 @@ _SIGS = {
     "lo_matmul_int4_int8": (None, [_P, _P, _P, _I, _I, _I, _I]),
     "lo_matmul_int8": (None, [_P, _P, _P, _I, _I, _I]),
     "lo_requantize_int32_to_int8": (None, [_P, _P, _SZ, _F, _F, ctypes.c_int32]),
+    "lo_quantize_int8_per_channel": (None, [_P, _P, _P, _SZ, ctypes.c_uint32, ctypes.c_uint32]),
+    "lo_dequantize_int8_per_channel": (None, [_P, _P, _P, _SZ, ctypes.c_uint32, ctypes.c_uint32]),
     "lo_apply_epilogue": (None, [_P, _I, _I, _I, _P, _P]),
     "lo_silu_mul": (None, [_P, _P, _I, _I]),
     "lo_rms_norm": (None, [_P, _P, _P, _P, _I, _I, _F]),
@@ -318,6 +320,37 @@ def requantize_int32_to_int8(x, in_scale, out_scale, out_zp=0) -> np.ndarray:
     out = np.empty(x.shape, np.int32)
     lib().lo_requantize_int32_to_int8(_p(x), _p(out), x.size, float(in_scale),
                                       float(out_scale), int(out_zp))
+    return out
+
+
+def channel_scales(scale, zero_point=None) -> np.ndarray:
+    """PerChannelScale array (quantized.wgsl:51-56): [C, 4] u32 words {f32 scale, i32
+    zero_point, 0, 0}."""
+    scale = np.asarray(scale, np.float32).ravel()
+    zp = np.zeros(scale.size, np.int32) if zero_point is None else np.asarray(zero_point, np.int32).ravel()
+    out = np.zeros((scale.size, 4), np.uint32)
+    out[:, 0] = scale.view(np.uint32)
+    out[:, 1] = zp.view(np.uint32)
+    return out
+
+
+def quantize_int8_per_channel(x, channels, stride, quant_type=0) -> np.ndarray:
+    """quantize_int8_per_channel (quantized.wgsl:264-280): i32 per element."""
+    x = _c(x, np.float32)
+    ch = _c(channels, np.uint32)
+    assert ch.shape[-1] == 4 and ch.shape[0] >= -(-x.size // stride)
+    out = np.empty(x.shape, np.int32)
+    lib().lo_quantize_int8_per_channel(_p(x), _p(ch), _p(out), x.size, int(stride), int(quant_type))
+    return out
+
+
+def dequantize_int8_per_channel(q, channels, stride, quant_type=0) -> np.ndarray:
+    """dequantize_int8_per_channel (quantized.wgsl:282-297): f32 per element."""
+    q = _c(q, np.int32)
+    ch = _c(channels, np.uint32)
+    assert ch.shape[-1] == 4 and ch.shape[0] >= -(-q.size // stride)
+    out = np.empty(q.shape, np.float32)
+    lib().lo_dequantize_int8_per_channel(_p(q), _p(ch), _p(out), q.size, int(stride), int(quant_type))
     return out
 
 

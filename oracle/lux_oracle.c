@@ -485,6 +485,42 @@ void lo_requantize_int32_to_int8(const int32_t* in, int32_t* out, size_t n, floa
     }
 }
 
+/* PerChannelScale (quantized.wgsl:51-56): {scale f32, zero_point i32, pad, pad}. */
+typedef struct {
+    float scale;
+    int32_t zero_point;
+    uint32_t pad0, pad1;
+} lo_channel_scale;
+
+/* quantized.wgsl:264-280 quantize_int8_per_channel: channel = i / channel_stride;
+ * quant_type 0 -> quantize_int8_symmetric (:83-86) clamp(i32(round(x / s)), -128, 127),
+ * otherwise quantize_int8_asymmetric (:92-95) clamp(i32(round(x / s) + f32(zp)), ...). */
+void lo_quantize_int8_per_channel(const float* in, const void* channels, int32_t* out, size_t n,
+                                  uint32_t stride, uint32_t quant_type) {
+    const lo_channel_scale* ch = (const lo_channel_scale*)channels;
+#pragma omp parallel for schedule(static)
+    for (size_t i = 0; i < n; ++i) {
+        const lo_channel_scale c = ch[i / stride];
+        float r = rintf(in[i] / c.scale);
+        if (quant_type != 0) r += (float)c.zero_point;
+        out[i] = clampi(f2i_sat(r), -128, 127);
+    }
+}
+
+/* quantized.wgsl:282-297 dequantize_int8_per_channel: quant_type 0 ->
+ * dequantize_int8_symmetric (:88-90) f32(q) * s, otherwise dequantize_int8_asymmetric
+ * (:97-99) f32(q - zp) * s, the i32 subtraction wrapping as WGSL's does. */
+void lo_dequantize_int8_per_channel(const int32_t* in, const void* channels, float* out, size_t n,
+                                    uint32_t stride, uint32_t quant_type) {
+    const lo_channel_scale* ch = (const lo_channel_scale*)channels;
+#pragma omp parallel for schedule(static)
+    for (size_t i = 0; i < n; ++i) {
+        const lo_channel_scale c = ch[i / stride];
+        const int32_t q = quant_type != 0 ? (int32_t)((uint32_t)in[i] - (uint32_t)c.zero_point) : in[i];
+        out[i] = (float)q * c.scale;
+    }
+}
+
 void lo_w4a8_group_partials(const uint32_t* W, const int8_t* A, int32_t* P, int M, int N, int K,
                             int gs, int coding) {
     int G = K / gs;

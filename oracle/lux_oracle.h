@@ -88,6 +88,14 @@ void lo_matmul_int4_int8(const uint32_t* W, const int8_t* act, int32_t* out, int
                          int nibble_coding);
 /* quantized.wgsl:497-555 matmul_int8. */
 void lo_matmul_int8(const int8_t* A, const int8_t* B, int32_t* out, int M, int N, int K);
+/* quantized.wgsl:264-280 / 282-297: per-channel int8 (i32 per element) with
+ * PerChannelScale {scale, zero_point, pad, pad} (:51-56) per channel_stride elements;
+ * quant_type 0 symmetric, otherwise asymmetric. */
+void lo_quantize_int8_per_channel(const float* in, const void* channels, int32_t* out, size_t n,
+                                  uint32_t stride, uint32_t quant_type);
+void lo_dequantize_int8_per_channel(const int32_t* in, const void* channels, float* out, size_t n,
+                                    uint32_t stride, uint32_t quant_type);
+
 /* quantized.wgsl:572-580 requantize_int32_to_int8. */
 void lo_requantize_int32_to_int8(const int32_t* in, int32_t* out, size_t n, float in_scale,
                                  float out_scale, int32_t out_zp);

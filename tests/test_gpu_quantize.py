@@ -229,6 +229,55 @@ def test_requantize_matches_oracle(ctx):
     assert ctx.download(ob, np.int32, t.shape).tolist() == [0, 2, 2, 0, -2]
 
 
+@pytest.mark.parametrize("size,stride", [(10001, 7), (4096 * 64, 4096), (1023, 1), (333, 1000)])
+@pytest.mark.parametrize("quant_type", [0, 1])
+def test_int8_per_channel_matches_oracle(ctx, size, stride, quant_type):
+    """quantize_int8_per_channel / dequantize_int8_per_channel (quantized.wgsl:264-297),
+    one i32 per element, bit-exact against the oracle; ragged sizes, a channel per element,
+    one channel for everything; half-even ties, saturation and NaN in the first elements."""
+    r = rng(size + stride)
+    C = -(-size // stride)
+    s = r.uniform(0.01, 0.1, size=C).astype(np.float32)
+    zp = r.integers(-20, 20, size=C).astype(np.int32)
+    ch = oracle.channel_scales(s, zp)
+    x = (r.standard_normal(size) * 8 * np.repeat(s, stride)[:size]).astype(np.float32)
+    x[:5] = [2.5 * s[0], -3.5 * s[0], 1e30, np.nan, -np.inf]  # ties exact in channel 0 (stride >= 2)
+    cb, xb, qb, ob = ctx.upload(ch), ctx.upload(x), ctx.alloc(size * 4), ctx.alloc(size * 4)
+    ctx.quantize_int8_per_channel(xb, cb, qb, size, stride, quant_type)
+    q = ctx.download(qb, np.int32, size)
+    assert np.array_equal(q, oracle.quantize_int8_per_channel(x, ch, stride, quant_type))
+    qi = r.integers(-128, 128, size=size).astype(np.int32)
+    qi[:2] = [-2**31, 2**31 - 1]  # the asymmetric subtraction wraps
+    ctx.dequantize_int8_per_channel(ctx.upload(qi), cb, ob, size, stride, quant_type)
+    got = ctx.download(ob, np.float32, size)
+    assert np.array_equal(got.view(np.uint32),
+                          oracle.dequantize_int8_per_channel(qi, ch, stride, quant_type).view(np.uint32))
+
+
+def test_int8_per_channel_unaligned_and_rejects(ctx):
+    """Buffers that are 4- but not 16-byte aligned take the element-wise path; bad
+    arguments are refused before any launch."""
+    import torch
+    size, stride = 1001, 10
+    r = rng(77)
+    ch = oracle.channel_scales(r.uniform(0.01, 0.1, size=-(-size // stride)).astype(np.float32))
+    x = r.standard_normal(size).astype(np.float32)
+    xt = torch.zeros(size + 1, dtype=torch.float32, device="cuda")
+    xt[1:] = torch.from_numpy(x).cuda()
+    qt = torch.zeros(size + 1, dtype=torch.int32, device="cuda")
+    cb = ctx.upload(ch)
+    ctx.quantize_int8_per_channel(ctx.wrap(xt[1:]), cb, ctx.wrap(qt[1:]), size, stride, 0)
+    torch.cuda.synchronize()
+    assert np.array_equal(qt[1:].cpu().numpy(), oracle.quantize_int8_per_channel(x, ch, stride, 0))
+    xb, qb = ctx.upload(x), ctx.alloc(size * 4)
+    with pytest.raises(W.LuxError) as e:
+        ctx.quantize_int8_per_channel(xb, cb, qb, size, 0, 0)
+    assert e.value.code == W.LUX_BACKEND_ERROR_INVALID_ARGUMENT
+    with pytest.raises(W.LuxError) as e:  # one PerChannelScale short
+        ctx.quantize_int8_per_channel(xb, ctx.upload(ch[:-1]), qb, size, stride, 0)
+    assert e.value.code == W.LUX_BACKEND_ERROR_INVALID_ARGUMENT
+
+
 def test_quantize_rejects(ctx):
     x = np.zeros((4, 96), np.float32)
     xb, qb, sb = ctx.upload(x), ctx.alloc(4 * 96), ctx.alloc(4 * 96 * 4)

@@ -301,6 +301,40 @@ def test_requantize():
     assert list(O.requantize_int32_to_int8(np.array([4, -300], np.int32), 1.0, 2.0, 3)) == [5, -128]
 
 
+def test_int8_per_channel_hand_vectors():
+    """quantize/dequantize_int8_per_channel (quantized.wgsl:264-297) on hand-computed
+    values: channel = i / stride (distinct scales per channel catch a wrong index), the
+    zero point's sign in both directions, half-to-even ties, i32 saturation, NaN -> 0 and
+    the wrapping i32 subtraction."""
+    ch = O.channel_scales([0.5, 2.0, 1.0], [3, -5, 1])
+    x = np.array([1.25, 1.75, -1.25, 5.0, 300.0, -1e30, np.nan], np.float32)
+    # x / s: 2.5, 3.5, -2.5 | 2.5, 150, -5e29 | NaN
+    assert O.quantize_int8_per_channel(x, ch, 3, 0).tolist() == [2, 4, -2, 2, 127, -128, 0]
+    assert O.quantize_int8_per_channel(x, ch, 3, 1).tolist() == [5, 7, 1, -3, 127, -128, 0]
+    assert O.quantize_int8_per_channel(x, ch, 3, 2).tolist() == [5, 7, 1, -3, 127, -128, 0]  # != 0: asym
+    q = np.array([2, -3, 127, 5, -128, 0, -2**31], np.int32)
+    assert O.dequantize_int8_per_channel(q, ch, 3, 0).tolist() == [1.0, -1.5, 63.5, 10.0, -256.0, 0.0,
+                                                                  -2147483648.0]
+    # asym: (q - zp) * s; -2^31 - 1 wraps to 2^31 - 1, whose f32 is 2^31
+    assert O.dequantize_int8_per_channel(q, ch, 3, 1).tolist() == [-0.5, -3.0, 62.0, 20.0, -246.0, 10.0,
+                                                                  2147483648.0]
+    # stride 1: every element its own channel; stride >= size: one channel
+    ch1 = O.channel_scales([1.0, 0.25, 4.0])
+    assert O.quantize_int8_per_channel(np.array([3.0, 3.0, 3.0], np.float32), ch1, 1).tolist() == [3, 12, 1]
+    assert O.quantize_int8_per_channel(np.array([3.0, 3.0, 3.0], np.float32), ch1, 100).tolist() == [3, 3, 3]
+
+
+def test_int8_per_channel_round_trip():
+    """Symmetric round trip: |dequantize(quantize(x)) - x| <= s / 2 for |x / s| <= 127."""
+    r = rng(12)
+    stride, C = 37, 11
+    s = r.uniform(0.01, 0.1, size=C).astype(np.float32)
+    x = (r.uniform(-120, 120, size=stride * C) * np.repeat(s, stride)).astype(np.float32)
+    ch = O.channel_scales(s)
+    back = O.dequantize_int8_per_channel(O.quantize_int8_per_channel(x, ch, stride), ch, stride)
+    assert np.all(np.abs(back.astype(np.float64) - x) <= np.repeat(s, stride).astype(np.float64) * 0.5 * (1 + 1e-6))
+
+
 # --------------------------------------------------------------------------- producers
 def test_group_scales_and_quantizers():
     r = rng(10)

@@ -158,6 +158,10 @@ EXPORTS = {
     "lux_hip_convert_scales": (c_int, [c_void_p, c_void_p, c_int, c_void_p, c_int, c_size_t]),
     "lux_hip_requantize_i32": (c_int, [c_void_p, c_void_p, c_void_p, c_size_t, c_float, c_float,
                                        c_int32]),
+    "lux_hip_quantize_int8_per_channel": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_size_t,
+                                                  c_uint32, c_uint32]),
+    "lux_hip_dequantize_int8_per_channel": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_size_t,
+                                                    c_uint32, c_uint32]),
     "lux_hip_gemv_f32": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, POINTER(GemvParams)]),
     "lux_hip_gemv_f32_batched": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p,
                                          POINTER(GemvBatchedParams)]),
@@ -442,6 +446,20 @@ class Context:
         self.plugin.check(self.lib.lux_hip_convert_scales(self.handle, src.handle, in_format,
                                                           dst.handle, out_format, count),
                           "convert_scales")
+
+    def quantize_int8_per_channel(self, src: Buffer, channel_scales: Buffer, dst: Buffer, size: int,
+                                  channel_stride: int, quant_type: int = 0):
+        """quantize_int8_per_channel (quantized.wgsl:264-280): f32 -> one i32 per element."""
+        self.plugin.check(self.lib.lux_hip_quantize_int8_per_channel(
+            self.handle, src.handle, channel_scales.handle, dst.handle, size, channel_stride, quant_type),
+            "quantize_int8_per_channel")
+
+    def dequantize_int8_per_channel(self, src: Buffer, channel_scales: Buffer, dst: Buffer, size: int,
+                                    channel_stride: int, quant_type: int = 0):
+        """dequantize_int8_per_channel (quantized.wgsl:282-297): i32 per element -> f32."""
+        self.plugin.check(self.lib.lux_hip_dequantize_int8_per_channel(
+            self.handle, src.handle, channel_scales.handle, dst.handle, size, channel_stride, quant_type),
+            "dequantize_int8_per_channel")
 
     def requantize(self, src: Buffer, dst: Buffer, size: int, input_scale: float,
                    output_scale: float, output_zero_point: int = 0):

@@ -333,6 +333,16 @@ hipError_t launch_dequantize(const QuantArgs& a, void* out, hipStream_t s);
 // out[i] = in[i] ^ mask over `words` u32 words (nibble re-coding; in == out allowed).
 hipError_t launch_xor_words(const void* in, void* out, size_t words, uint32_t mask, hipStream_t s);
 hipError_t launch_convert_scales(const void* in, ScaleKind ik, void* out, ScaleKind ok, size_t n, hipStream_t s);
+// PerChannelScale of quantized.wgsl:51-56.
+struct ChannelScale {
+    float scale;
+    int32_t zero_point;
+    uint32_t pad0, pad1;
+};
+// quantize_int8_per_channel (f32 -> i32) or dequantize_int8_per_channel (i32 -> f32),
+// quantized.wgsl:264-297; asym: quant_type != 0.  Buffers 4-byte aligned.
+hipError_t launch_int8_per_channel(bool dequantize, const void* in, const ChannelScale* ch, void* out, size_t n,
+                                  uint32_t stride, bool asym, hipStream_t s);
 hipError_t launch_requantize(const int32_t* in, int32_t* out, size_t n, float s_in, float s_out, int32_t zp,
                              hipStream_t s);
 

@@ -931,6 +931,44 @@ LUX_EXPORT LuxBackendError lux_hip_rms_norm(LuxBackendContext* ctx, const LuxHip
                   "rms_norm");
 }
 
+// quantize_int8_per_channel / dequantize_int8_per_channel (quantized.wgsl:264-297):
+// QuantParams.size and .quant_type (:37-42), ChannelQuantParams.channel_stride (:44-49),
+// channel_scales: PerChannelScale[ceil(size / channel_stride)] (:51-56).
+static LuxBackendError int8_per_channel(LuxBackendContext* ctx, bool dequantize, LuxBackendBuffer* in,
+                                        LuxBackendBuffer* channel_scales, LuxBackendBuffer* out, size_t size,
+                                        uint32_t channel_stride, uint32_t quant_type) {
+    const char* op = dequantize ? "dequantize_int8_per_channel" : "quantize_int8_per_channel";
+    HipCtx* c = C(ctx);
+    HipBuf *I = B(in), *S = B(channel_scales), *O = B(out);
+    if (!c || !I || !S || !O) return fail(LUX_BACKEND_ERROR_INVALID_ARGUMENT, "%s: NULL argument", op);
+    if (channel_stride == 0) return fail(LUX_BACKEND_ERROR_INVALID_ARGUMENT, "%s: channel_stride is 0", op);
+    const size_t channels = size / channel_stride + (size % channel_stride != 0);
+    if (!fits(I, size * 4) || !fits(O, size * 4) || !fits(S, channels * sizeof(ChannelScale)))
+        return fail(LUX_BACKEND_ERROR_INVALID_ARGUMENT, "%s: buffer too small", op);
+    if (((uintptr_t)I->ptr | (uintptr_t)O->ptr | (uintptr_t)S->ptr) & 3u)
+        return fail(LUX_BACKEND_ERROR_NOT_SUPPORTED, "%s: buffers must be 4-byte aligned", op);
+    if (LuxBackendError e = begin_op(c, op)) return e;
+    if (size == 0) return LUX_BACKEND_OK;
+    return end_op(c,
+                  launch_int8_per_channel(dequantize, I->ptr, static_cast<const ChannelScale*>(S->ptr), O->ptr, size,
+                                          channel_stride, quant_type != 0, c->stream),
+                  op);
+}
+
+LUX_EXPORT LuxBackendError lux_hip_quantize_int8_per_channel(LuxBackendContext* ctx, LuxBackendBuffer* in,
+                                                             LuxBackendBuffer* channel_scales,
+                                                             LuxBackendBuffer* out, size_t size,
+                                                             uint32_t channel_stride, uint32_t quant_type) {
+    return int8_per_channel(ctx, false, in, channel_scales, out, size, channel_stride, quant_type);
+}
+
+LUX_EXPORT LuxBackendError lux_hip_dequantize_int8_per_channel(LuxBackendContext* ctx, LuxBackendBuffer* in,
+                                                               LuxBackendBuffer* channel_scales,
+                                                               LuxBackendBuffer* out, size_t size,
+                                                               uint32_t channel_stride, uint32_t quant_type) {
+    return int8_per_channel(ctx, true, in, channel_scales, out, size, channel_stride, quant_type);
+}
+
 // requantize_int32_to_int8 (quantized.wgsl:560-580): RequantParams {size, input_scale,
 // output_scale, output_zero_point}; i32 in, i32 out clamped to [-128, 127].
 LUX_EXPORT LuxBackendError lux_hip_requantize_i32(LuxBackendContext* ctx, LuxBackendBuffer* in,

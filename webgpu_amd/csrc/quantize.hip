@@ -310,6 +310,61 @@ __global__ __launch_bounds__(256) void k_requantize(const int32_t* __restrict__ 
     out[i] = min(max(f2i_sat(r), -128), 127);
 }
 
+// quantize_int8_per_channel / dequantize_int8_per_channel (quantized.wgsl:264-297): one
+// i32 per element and a 16-byte PerChannelScale {scale, zero_point, pad, pad} (:51-56)
+// per channel_stride elements; quant_type 0 is the symmetric branch, any other value the
+// asymmetric one.  HBM-bound (8 bytes per element); a thread takes 4 consecutive
+// elements (16-byte accesses when both buffers are 16-byte aligned) and divides once for
+// the channel of the first.
+//   quantize:   q = clamp(i32(round(x / s) [+ f32(zp)]), -128, 127)   (:83-86, :92-95)
+//   dequantize: x = f32(q [- zp]) * s, the i32 subtraction wrapping      (:88-90, :97-99)
+template <bool DEQ, bool VEC>
+__global__ __launch_bounds__(256) void k_int8_per_channel(const void* __restrict__ in,
+                                                          const ChannelScale* __restrict__ ch,
+                                                          void* __restrict__ out, size_t n, uint32_t stride,
+                                                          int asym) {
+    const size_t i0 = ((size_t)blockIdx.x * 256 + threadIdx.x) * 4;
+    if (i0 >= n) return;
+    size_t c = i0 / stride;
+    uint32_t rem = (uint32_t)(i0 - c * stride);
+    ChannelScale cs = ch[c];
+    uint32_t v[4] = {0u, 0u, 0u, 0u};
+    const bool full = VEC && i0 + 4 <= n;
+    if (full) {
+        const u32x4 w = reinterpret_cast<const u32x4*>(in)[i0 / 4];
+        v[0] = w.x, v[1] = w.y, v[2] = w.z, v[3] = w.w;
+    } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            if (i0 + e < n) v[e] = reinterpret_cast<const uint32_t*>(in)[i0 + e];
+    }
+    uint32_t o[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        if (rem == stride) {  // next channel
+            ++c;
+            rem = 0;
+            if (i0 + e < n) cs = ch[c];
+        }
+        ++rem;
+        if constexpr (DEQ) {
+            const int32_t q = asym ? (int32_t)(v[e] - (uint32_t)cs.zero_point) : (int32_t)v[e];
+            o[e] = __builtin_bit_cast(uint32_t, (float)q * cs.scale);
+        } else {
+            float r = rintf(__builtin_bit_cast(float, v[e]) / cs.scale);
+            if (asym) r += (float)cs.zero_point;
+            o[e] = (uint32_t)min(max(f2i_sat(r), -128), 127);
+        }
+    }
+    if (full) {
+        reinterpret_cast<u32x4*>(out)[i0 / 4] = u32x4{o[0], o[1], o[2], o[3]};
+    } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            if (i0 + e < n) reinterpret_cast<uint32_t*>(out)[i0 + e] = o[e];
+    }
+}
+
 // ---------------------------------------------------------------------------- host
 
 // Dequantizer, 8-weight chunks (one int4 word or two int8 words; group_size % 8 == 0, so
@@ -458,6 +513,22 @@ hipError_t launch_convert_scales(const void* in, ScaleKind ik, void* out, ScaleK
         case ScaleKind::GroupScale: return launch_cs<ScaleKind::GroupScale>(in, out, ok, n, s);
         default: return hipErrorInvalidValue;
     }
+}
+
+hipError_t launch_int8_per_channel(bool dequantize, const void* in, const ChannelScale* ch, void* out, size_t n,
+                                  uint32_t stride, bool asym, hipStream_t s) {
+    if (n == 0) return hipSuccess;
+    const bool vec = ((uintptr_t)in & 15u) == 0 && ((uintptr_t)out & 15u) == 0;
+    const dim3 grid((unsigned)((n + 1023) / 1024)), block(256);
+    const int a = asym ? 1 : 0;
+    if (dequantize) {
+        if (vec) hipLaunchKernelGGL((k_int8_per_channel<true, true>), grid, block, 0, s, in, ch, out, n, stride, a);
+        else hipLaunchKernelGGL((k_int8_per_channel<true, false>), grid, block, 0, s, in, ch, out, n, stride, a);
+    } else {
+        if (vec) hipLaunchKernelGGL((k_int8_per_channel<false, true>), grid, block, 0, s, in, ch, out, n, stride, a);
+        else hipLaunchKernelGGL((k_int8_per_channel<false, false>), grid, block, 0, s, in, ch, out, n, stride, a);
+    }
+    return hipGetLastError();
 }
 
 hipError_t launch_requantize(const int32_t* in, int32_t* out, size_t n, float s_in, float s_out, int32_t zp,

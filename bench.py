@@ -399,7 +399,8 @@ def bench_gemm_f32(torch, W, ctx, n, steps, warmup):
     tf = 2.0 * n * n * n / per / 1e12
     return {"n": n, "us_per_launch": round(per * 1e6, 2), "value": round(tf, 2), "unit": "TFLOP/s",
             "roofline": {"bound": "mfma", "achieved": round(tf, 2), "peak": MFMA_F32_PEAK_TFLOPS,
-                         "unit": "TFLOP/s", "frac": round(tf / MFMA_F32_PEAK_TFLOPS, 4), "traffic": None}}
+                         "unit": "TFLOP/s", "frac": round(tf / MFMA_F32_PEAK_TFLOPS, 4),
+                         "traffic": measured_traffic(f"gemm{n}")}}
 
 
 GH_BYTES = 14336 * 4096 * 2 + 4096 * 2 + 14336 * 4  # A (f16) + x read, y (f32) written

@@ -535,22 +535,20 @@ void k_qgemm_i4_xr(const f16* __restrict__ X, const float* __restrict__ xfac,
             R.sr[t] = load_scale_raw<SK>(S, (size_t)srow * G + (k0 + 32 * (SPT * wh + t)) / gs);
         }
     };
-    auto store_w = [&](const Regs& R, int buf) {
+    // Word q (8 weights) of every slice of the next stage: called once per k-step with
+    // q = kk % 4, so the dequantisation is spread over the stage's MFMAs instead of
+    // arriving in one burst (the two waves of a SIMD reach each k-step together).
+    auto store_w = [&](const Regs& R, int buf, int q) {
 #pragma unroll
         for (int t = 0; t < SPT; ++t) {
             f16* wb = ws + buf * TBN * LR + wr_row * LR + 32 * (SPT * wh + t);
-            const uint32_t words[4] = {R.wr[t].x, R.wr[t].y, R.wr[t].z, R.wr[t].w};
+            const uint32_t word = (q == 0 ? R.wr[t].x : q == 1 ? R.wr[t].y : q == 2 ? R.wr[t].z : R.wr[t].w) ^ xor_mask;
             if constexpr (SK == ScaleKind::F16) {
                 const f16 sc = (f16)(scale_from_raw<SK>(R.sr[t]) * winv);
-                const f16x2 s2 = {sc, sc};
-#pragma unroll
-                for (int q = 0; q < 4; ++q)
-                    *reinterpret_cast<u32x4*>(wb + 8 * q) = dequant8(words[q] ^ xor_mask, s2, magic);
+                *reinterpret_cast<u32x4*>(wb + 8 * q) = dequant8(word, f16x2{sc, sc}, magic);
             } else {
                 const float sc = scale_from_raw<SK>(R.sr[t]) * winv;
-#pragma unroll
-                for (int q = 0; q < 4; ++q)
-                    *reinterpret_cast<u32x4*>(wb + 8 * q) = dequant8_f32s(words[q] ^ xor_mask, sc);
+                *reinterpret_cast<u32x4*>(wb + 8 * q) = dequant8_f32s(word, sc);
             }
         }
     };
@@ -593,8 +591,19 @@ void k_qgemm_i4_xr(const f16* __restrict__ X, const float* __restrict__ xfac,
                 for (int i = 0; i < 2; ++i)
                     acc[j][i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(b[kk & 1][j], xf[kk][i], acc[j][i], 0, 0, 0);
             load_x(kk, NKK * (s + 1) + kk);
-            __builtin_amdgcn_sched_barrier(0);  // issue here: the scheduler would sink loads to the barrier
-            if (kk == 0) store_w(nxt, buf ^ 1);
+            store_w(nxt, buf ^ 1, kk & 3);
+            // Issue order of the k-step: the next k-step's weight fragments, then each MFMA
+            // followed by two VALU ops of the dequantisation, then the X loads and the LDS
+            // store.  The barrier closes the k-step, so no load sinks to the stage's end.
+            __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);  // DS reads
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+                __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);  // VALU
+            }
+            __builtin_amdgcn_sched_group_barrier(0x020, 2, 0);  // VMEM reads
+            __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);  // DS write
+            __builtin_amdgcn_sched_barrier(0);
         }
     };
 
@@ -604,7 +613,8 @@ void k_qgemm_i4_xr(const f16* __restrict__ X, const float* __restrict__ xfac,
     for (int kk = 0; kk < NKK; ++kk) load_x(kk, kk);
     load_w(R0, 0);
     load_w(R1, KB);
-    store_w(R0, 0);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) store_w(R0, 0, q);
     __syncthreads();
     const int npairs = nstages >> 1;
     for (int p = 0; p < npairs; ++p) {

@@ -466,27 +466,29 @@ void k_qgemm_i4_large(const f16* __restrict__ X, const float* __restrict__ xfac,
 
 // The same GEMM with the activation operand read straight from X staged in fragment
 // order (k_x_to_f16_frag) into MFMA registers, one contiguous 1 KB per fragment, so only
-// the dequantised weights pass through LDS.  Waves tile 4 (m) x 2 (n), 64 x 128 each: per
-// 64-k stage the block writes 32 KB of weights to LDS and its waves read 128 KB of weight
-// fragments, against 64 KB and 192 KB when both operands are staged; the two waves that
-// share a row range read the same X lines, which L1 and L2 serve.  The MFMA sequence per
-// output element is the staged kernel's, so the results are identical.  Measured on
-// config 4: 2-3 % faster than the staged kernel (the pre-pass costs 0.9 us more).
-template <ScaleKind SK, YKind YK, int KB>
+// the dequantised weights pass through LDS.  8 waves in a 4 (m) x 2 (n) grid, each with
+// TM x TN tiles of 32 x 32: TM = 2, TN = 4 gives a 256 x 256 block tile, TM = 4, TN = 2 a
+// 512 x 128 one (each weight tile dequantised once per 512 rows of X, half as often, for
+// twice the X fragment loads).  The MFMA sequence per output element is the staged
+// kernel's, so the results are identical.
+template <ScaleKind SK, YKind YK, int TM, int TN, int WGM = 4>
 __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void k_qgemm_i4_xr(const f16* __restrict__ X, const float* __restrict__ xfac,
                    const uint32_t* __restrict__ W, const void* __restrict__ S,
                    const float* __restrict__ wfold, void* __restrict__ Y,
                    int M, int N, int K, int gs, uint32_t xor_mask, int vec_y, EpiArgs epi) {
-    // KB k per stage (64 or 128); LDS rows of KB + 8 halves keep the b128 reads conflict-free
-    constexpr int LR = KB + 8, NKK = KB / 16, SPT = KB / 64;  // k-steps per stage, 32-k slices per thread
-    constexpr int NTH = NT, TBN = BN;
+    constexpr int WGN = 8 / WGM;                    // waves in m and n
+    constexpr int TBM = 32 * TM * WGM, TBN = 32 * TN * WGN;  // block tile
+    constexpr int NKK = BK / 16;                    // k-steps per 64-k stage
+    constexpr int TPR = NT / TBN, KPT = BK / TPR;   // threads per weight row, k per thread
+    constexpr int WPT = KPT / 8;                    // packed words (8 weights) per thread
+    constexpr int HALF = 16 * TN;                   // SiluMul: gate rows per wave
     extern __shared__ __attribute__((aligned(16))) f16 lds[];
-    f16* ws = lds;  // [2][BN][LR]
+    f16* ws = lds;  // [2][TBN][LDS_ROW]
 
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-    const int wm = wv >> 1, wn = wv & 1;  // wave tile: 64 (m) x 128 (n)
-    const int m0 = blockIdx.y * BM, n0 = blockIdx.x * TBN;
+    const int wm = wv / WGN, wn = wv % WGN;  // wave tile: 32 TM (m) x 32 TN (n)
+    const int m0 = blockIdx.y * TBM, n0 = blockIdx.x * TBN;
     const int G = K / gs;
 
     const uint32_t xbytes = (uint32_t)((size_t)(M + 31) / 32 * 32 * K * 2), wbytes = (uint32_t)((size_t)N * K / 2);
@@ -499,57 +501,61 @@ void k_qgemm_i4_xr(const f16* __restrict__ X, const float* __restrict__ xfac,
     // (ceil(M / 32) of them) read zeros.
     const int kofs = (lane >> 5) * 8;
     const int mtiles = (M + 31) / 32;
-    uint32_t xoff[2];
+    uint32_t xoff[TM];
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        const int mt = (m0 >> 5) + 2 * wm + i;
+    for (int i = 0; i < TM; ++i) {
+        const int mt = (m0 >> 5) + TM * wm + i;
         xoff[i] = mt < mtiles ? (uint32_t)((size_t)mt * (K / 16) * 1024 + 16 * lane) : xbytes;
     }
-    // Weight row of LDS row rho.  SiluMul: wave wn's 128 rows are 64 gate rows g0 + 64 wn ..
-    // (tiles j = 0, 1) and the matching up rows (tiles j = 2, 3), g0 = 128 blockIdx.x.
+    // Weight row of LDS row rho.  SiluMul: wave wn's 32 TN rows are HALF gate rows
+    // g0 + HALF wn .. (tiles j < TN / 2) and the matching up rows (tiles j + TN / 2),
+    // g0 = blockIdx.x * TBN / 2.
     const bool sm = epi.kind == (int)Epi::SiluMul;
     const int nh = N / 2, g0 = blockIdx.x * (TBN / 2);
     auto grow = [&](int rho) {  // -1: past the end
         if (!sm) return n0 + rho < N ? n0 + rho : -1;
-        const int w = rho >> 7, o = rho & 127, g = g0 + 64 * w + (o & 63);
-        return g < nh ? (o < 64 ? g : nh + g) : -1;
+        const int w = rho / (2 * HALF), o = rho % (2 * HALF), g = g0 + HALF * w + o % HALF;
+        return g < nh ? (o < HALF ? g : nh + g) : -1;
     };
-    // W: 2 threads per row of the n tile; thread t takes row t / 2 and SPT 32-k slices
-    // (16 B of nibbles and one g32 scale each) from k = KB / 2 * (t % 2).
-    const int wr_row = tid >> 1, wh = tid & 1;
+    // W: TPR threads per row of the n tile; thread t takes row t / TPR and KPT k (WPT words
+    // of nibbles, inside one g32 group) from k = KPT * (t % TPR).
+    const int wr_row = tid / TPR, wh = tid % TPR;
     const int wgr = grow(wr_row);
-    const uint32_t woff = wgr >= 0 ? (uint32_t)((size_t)wgr * (K / 2) + 16 * SPT * wh) : wbytes;
+    const uint32_t woff = wgr >= 0 ? (uint32_t)((size_t)wgr * (K / 2) + KPT / 2 * wh) : wbytes;
     const int srow = wgr >= 0 ? wgr : N - 1;
     const float winv = 1.0f / wfold[srow];  // exact: the fold is a power of two
     const uint32_t magic = 0x64006400u;
 
     struct Regs {
-        u32x4 wr[SPT];
-        uint32_t sr[SPT];
+        uint32_t w[WPT];
+        uint32_t sr;
     };
+    static_assert(WPT == 1 || WPT == 2 || WPT == 4, "8, 16 or 32 k per thread");
     auto load_w = [&](Regs& R, int k0) {
-        k0 = __builtin_amdgcn_readfirstlane(min(k0, K - KB));
-#pragma unroll
-        for (int t = 0; t < SPT; ++t) {
-            R.wr[t] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rw, (int)woff + 16 * t, k0 / 2, 0));
-            R.sr[t] = load_scale_raw<SK>(S, (size_t)srow * G + (k0 + 32 * (SPT * wh + t)) / gs);
+        k0 = __builtin_amdgcn_readfirstlane(min(k0, K - BK));
+        if constexpr (WPT == 4) {
+            const u32x4 v = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rw, (int)woff, k0 / 2, 0));
+            R.w[0] = v.x, R.w[1] = v.y, R.w[2] = v.z, R.w[3] = v.w;
+        } else if constexpr (WPT == 1) {
+            R.w[0] = __builtin_amdgcn_raw_buffer_load_b32(rw, (int)woff, k0 / 2, 0);
+        } else {
+            const u32x2 v = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(rw, (int)woff, k0 / 2, 0));
+            R.w[0] = v.x, R.w[1] = v.y;
         }
+        R.sr = load_scale_raw<SK>(S, (size_t)srow * G + (k0 + KPT * wh) / gs);
     };
-    // Word q (8 weights) of every slice of the next stage: called once per k-step with
-    // q = kk % 4, so the dequantisation is spread over the stage's MFMAs instead of
-    // arriving in one burst (the two waves of a SIMD reach each k-step together).
+    // Word q (8 weights) of the next stage, one per k-step (WPT = 4) or every other k-step
+    // (WPT = 2), so the dequantisation is spread over the stage's MFMAs instead of arriving
+    // in one burst (the two waves of a SIMD reach each k-step together).
     auto store_w = [&](const Regs& R, int buf, int q) {
-#pragma unroll
-        for (int t = 0; t < SPT; ++t) {
-            f16* wb = ws + buf * TBN * LR + wr_row * LR + 32 * (SPT * wh + t);
-            const uint32_t word = (q == 0 ? R.wr[t].x : q == 1 ? R.wr[t].y : q == 2 ? R.wr[t].z : R.wr[t].w) ^ xor_mask;
-            if constexpr (SK == ScaleKind::F16) {
-                const f16 sc = (f16)(scale_from_raw<SK>(R.sr[t]) * winv);
-                *reinterpret_cast<u32x4*>(wb + 8 * q) = dequant8(word, f16x2{sc, sc}, magic);
-            } else {
-                const float sc = scale_from_raw<SK>(R.sr[t]) * winv;
-                *reinterpret_cast<u32x4*>(wb + 8 * q) = dequant8_f32s(word, sc);
-            }
+        f16* wb = ws + buf * TBN * LDS_ROW + wr_row * LDS_ROW + KPT * wh + 8 * q;
+        const uint32_t word = R.w[q] ^ xor_mask;
+        if constexpr (SK == ScaleKind::F16) {
+            const f16 sc = (f16)(scale_from_raw<SK>(R.sr) * winv);
+            *reinterpret_cast<u32x4*>(wb) = dequant8(word, f16x2{sc, sc}, magic);
+        } else {
+            const float sc = scale_from_raw<SK>(R.sr) * winv;
+            *reinterpret_cast<u32x4*>(wb) = dequant8_f32s(word, sc);
         }
     };
     // X fragments, one register set per k-step of a stage: right after the MFMAs of k-step
@@ -558,72 +564,74 @@ void k_qgemm_i4_xr(const f16* __restrict__ X, const float* __restrict__ xfac,
     // of stage s, so X loaded only a few k-steps ahead would make each k-step wait for HBM;
     // a stage ahead, both loads get a stage of latency.
     const int nks = K / 16;
-    f16x8 xf[NKK][2];
+    f16x8 xf[NKK][TM];
     auto load_x = [&](int kk, int gk) {
         const int so = __builtin_amdgcn_readfirstlane(min(gk, nks - 1) * 1024);
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
+        for (int i = 0; i < TM; ++i)
             xf[kk][i] = __builtin_bit_cast(f16x8, __builtin_amdgcn_raw_buffer_load_b128(rx, (int)xoff[i], so, 0));
     };
 
-    f32x16 acc[4][2];
+    f32x16 acc[TN][TM];
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+    for (int j = 0; j < TN; ++j)
 #pragma unroll
-        for (int i = 0; i < 2; ++i) acc[j][i] = f32x16{};
+        for (int i = 0; i < TM; ++i) acc[j][i] = f32x16{};
 
-    const int brow = wn * 128 + (lane & 31);
+    const int brow = wn * 32 * TN + (lane & 31);
     auto compute = [&](int buf, const Regs& nxt, int s) {
-        const f16* wb = ws + buf * TBN * LR;
-        f16x8 b[2][4];
-        auto read_w = [&](int kk, f16x8 (&bv)[4]) {
+        const f16* wb = ws + buf * TBN * LDS_ROW;
+        f16x8 b[2][TN];
+        auto read_w = [&](int kk, f16x8 (&bv)[TN]) {
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
-                bv[j] = *reinterpret_cast<const f16x8*>(wb + (brow + 32 * j) * LR + 16 * kk + kofs);
+            for (int j = 0; j < TN; ++j)
+                bv[j] = *reinterpret_cast<const f16x8*>(wb + (brow + 32 * j) * LDS_ROW + 16 * kk + kofs);
         };
         read_w(0, b[0]);
 #pragma unroll
         for (int kk = 0; kk < NKK; ++kk) {
             if (kk + 1 < NKK) read_w(kk + 1, b[(kk + 1) & 1]);
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
+            for (int j = 0; j < TN; ++j)
 #pragma unroll
-                for (int i = 0; i < 2; ++i)
+                for (int i = 0; i < TM; ++i)
                     acc[j][i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(b[kk & 1][j], xf[kk][i], acc[j][i], 0, 0, 0);
             load_x(kk, NKK * (s + 1) + kk);
-            store_w(nxt, buf ^ 1, kk & 3);
+            if (WPT == 4) store_w(nxt, buf ^ 1, kk);
+            else if (WPT == 2 && (kk & 1) == 0) store_w(nxt, buf ^ 1, kk >> 1);
+            else if (WPT == 1 && kk == 0) store_w(nxt, buf ^ 1, 0);
             // Issue order of the k-step: the next k-step's weight fragments, then each MFMA
             // followed by two VALU ops of the dequantisation, then the X loads and the LDS
             // store.  The barrier closes the k-step, so no load sinks to the stage's end.
-            __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);  // DS reads
+            __builtin_amdgcn_sched_group_barrier(0x100, TN, 0);  // DS reads
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
                 __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
                 __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);  // VALU
             }
-            __builtin_amdgcn_sched_group_barrier(0x020, 2, 0);  // VMEM reads
-            __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);  // DS write
+            __builtin_amdgcn_sched_group_barrier(0x020, TM, 0);  // VMEM reads
+            __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);   // DS write
             __builtin_amdgcn_sched_barrier(0);
         }
     };
 
-    const int nstages = K / KB;
+    const int nstages = K / BK;
     Regs R0, R1;
 #pragma unroll
     for (int kk = 0; kk < NKK; ++kk) load_x(kk, kk);
     load_w(R0, 0);
-    load_w(R1, KB);
+    load_w(R1, BK);
 #pragma unroll
-    for (int q = 0; q < 4; ++q) store_w(R0, 0, q);
+    for (int q = 0; q < WPT; ++q) store_w(R0, 0, q);
     __syncthreads();
     const int npairs = nstages >> 1;
     for (int p = 0; p < npairs; ++p) {
         const int s = 2 * p;
-        load_w(R0, (s + 2) * KB);
+        load_w(R0, (s + 2) * BK);
         __builtin_amdgcn_sched_barrier(0);
         compute(0, R1, s);  // stores stage s+1 into buffer 1
         __syncthreads();
-        load_w(R1, (s + 3) * KB);
+        load_w(R1, (s + 3) * BK);
         __builtin_amdgcn_sched_barrier(0);
         compute(1, R0, s + 1);  // stores stage s+2 into buffer 0
         __syncthreads();
@@ -632,13 +640,13 @@ void k_qgemm_i4_xr(const f16* __restrict__ X, const float* __restrict__ xfac,
 
     __syncthreads();
     float* fac = reinterpret_cast<float*>(lds);
-    float* wf = fac + BM;
-    for (int t = tid; t < BM + TBN; t += NTH) {
-        if (t < BM) {
+    float* wf = fac + TBM;
+    for (int t = tid; t < TBM + TBN; t += NT) {
+        if (t < TBM) {
             fac[t] = m0 + t < M ? xfac[m0 + t] : 0.0f;
         } else {
-            const int g = grow(t - BM);
-            wf[t - BM] = g >= 0 ? wfold[g] : 1.0f;
+            const int g = grow(t - TBM);
+            wf[t - TBM] = g >= 0 ? wfold[g] : 1.0f;
         }
     }
     __syncthreads();
@@ -647,23 +655,23 @@ void k_qgemm_i4_xr(const f16* __restrict__ X, const float* __restrict__ xfac,
     // c + 32 * ((r / 4) & 1), register 4 * (r / 8) + r % 4.
     const bool vec = vec_y != 0;
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        const int ml = wm * 64 + 32 * i + (lane & 31);
+    for (int i = 0; i < TM; ++i) {
+        const int ml = wm * 32 * TM + 32 * i + (lane & 31);
         const int m = m0 + ml;
         if (m >= M) continue;
         const float fm = fac[ml];
-        if (sm) {  // silu(gate) * up: gate tiles j = 0, 1, up tiles j + 2, output [M x nh]
+        if (sm) {  // silu(gate) * up: gate tiles j < TN / 2, up tiles j + TN / 2, output [M x nh]
 #pragma unroll
-            for (int j = 0; j < 2; ++j)
+            for (int j = 0; j < TN / 2; ++j)
 #pragma unroll
                 for (int g = 0; g < 4; ++g) {
-                    const int n = g0 + wn * 64 + 32 * j + 8 * g + 4 * (lane >> 5);
+                    const int n = g0 + wn * HALF + 32 * j + 8 * g + 4 * (lane >> 5);
                     f32x4 v;
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
-                        const int rho = wn * 128 + 32 * j + 8 * g + 4 * (lane >> 5) + r;  // its up row: rho + 64
+                        const int rho = wn * 32 * TN + 32 * j + 8 * g + 4 * (lane >> 5) + r;  // its up row: rho + HALF
                         v[r] = silu_f(acc[j][i][4 * g + r] * fm * wf[rho]) *
-                               (acc[j + 2][i][4 * g + r] * fm * wf[rho + 64]);
+                               (acc[j + TN / 2][i][4 * g + r] * fm * wf[rho + HALF]);
                     }
                     if (vec && n + 3 < nh) {
                         store_y4<YK>(Y, (size_t)m * nh + n, v);
@@ -676,10 +684,10 @@ void k_qgemm_i4_xr(const f16* __restrict__ X, const float* __restrict__ xfac,
             continue;
         }
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
+        for (int j = 0; j < TN; ++j)
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
-                const int rho = wn * 128 + 32 * j + 8 * g + 4 * (lane >> 5);
+                const int rho = wn * 32 * TN + 32 * j + 8 * g + 4 * (lane >> 5);
                 const int n = n0 + rho;
                 f32x4 v = f32x4{acc[j][i][4 * g] * wf[rho], acc[j][i][4 * g + 1] * wf[rho + 1],
                                 acc[j][i][4 * g + 2] * wf[rho + 2], acc[j][i][4 * g + 3] * wf[rho + 3]} * fm;
@@ -726,16 +734,16 @@ static void launch_t(const QArgs& a, const f16* xst, const float* xfac, const fl
     static bool attr = [] {
         (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&k_qgemm_i4_large<SK, YK>),
                                   hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
-        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&k_qgemm_i4_xr<SK, YK, BK>),
-                                  hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+
 
         return true;
     }();
     (void)attr;
     const int vy = (ny % 4 == 0 && ((uintptr_t)a.y & 15u) == 0) ? 1 : 0;
-    if (xr) {
-        const size_t lds = (size_t)2 * BN * (BK + 8) * sizeof(f16);
-        hipLaunchKernelGGL((k_qgemm_i4_xr<SK, YK, BK>), grid, block, lds, s, xst, xfac,
+    if (xr) {  // 512 x 128 block tiles
+        const dim3 xgrid(sm ? (ny + 63) / 64 : (a.n_out + 127) / 128, (a.m + 511) / 512);
+        const size_t lds = (size_t)2 * 128 * LDS_ROW * sizeof(f16);
+        hipLaunchKernelGGL((k_qgemm_i4_xr<SK, YK, 4, 2>), xgrid, block, lds, s, xst, xfac,
                            reinterpret_cast<const uint32_t*>(a.w), a.s, wfold, a.y, a.m, a.n_out, a.k,
                            a.group_size, a.xor_mask, vy, a.epi);
         return;

@@ -436,15 +436,16 @@ FFN = dict(hidden=4096, inter=14336, gs=32)
 def ffn_bytes():
     h, i, gs = FFN["hidden"], FFN["inter"], FFN["gs"]
     w = 2 * i * h // 2 + 2 * i * (h // gs) * 2 + h * i // 2 + h * (i // gs) * 2  # int4 + fp16 scales
-    act = h * 4 * 2 + h * 4 + h * 2 * 2 + i * 2 * 2 + h * 4  # x (twice), gamma, normed, h, x_next
+    act = h * 4 * 2 + h * 4 + i * 2 * 2 + h * 4  # x (twice), gamma, h (written, read), x_next
     return w + act
 
 
 def bench_ffn(torch, W, ctx, steps, warmup):
-    """One decode step of a gated FFN through the plugin: rms_norm (f32 -> f16), int4 g32
-    gate/up GEMV with the SILU_MUL epilogue (2 x 14336 x 4096), int4 g32 down GEMV
-    (4096 x 14336) with the residual added in its ADD_RESIDUAL epilogue: three launches.
-    Weights rotate over copies beyond the MALL."""
+    """One decode step of a gated FFN through the plugin: rms_norm (f32 -> f16) fused into
+    the int4 g32 gate/up GEMV with the SILU_MUL epilogue (2 x 14336 x 4096,
+    lux_hip_rms_norm_qmatmul), then the int4 g32 down GEMV (4096 x 14336) with the
+    residual added in its ADD_RESIDUAL epilogue: two launches.  Weights rotate over copies
+    beyond the MALL."""
     from util import int4_weights
     h, i, gs = FFN["hidden"], FFN["inter"], FFN["gs"]
     r = np.random.default_rng(45)
@@ -457,19 +458,18 @@ def bench_ffn(torch, W, ctx, steps, warmup):
     s_d = [ctx.upload(sd) for _ in range(copies)]
     x = ctx.upload(r.standard_normal(h).astype(np.float32))
     gamma = ctx.upload(r.uniform(0.8, 1.2, h).astype(np.float32))
-    nb, hb, xn = ctx.alloc(h * 2), ctx.alloc(i * 2), ctx.alloc(h * 4)
+    hb, xn = ctx.alloc(i * 2), ctx.alloc(h * 4)
     d_gu = W.qdesc(2 * i, h, 1, 4, gs, 0, W.SCALE_F16, W.F16, W.F16)
     d_d = W.qdesc(h, i, 1, 4, gs, 0, W.SCALE_F16, W.F16, W.F32)
 
     def launch(j):
         k = j % copies
-        ctx.rms_norm(x, gamma, nb, 1, h, 1e-6, W.F32, W.F16)
-        ctx.qmatmul_ex(d_gu, wgu[k], s_gu[k], nb, None, W.EPI_SILU_MUL, None, None, hb)
+        ctx.rms_norm_qmatmul(x, gamma, 1e-6, W.F32, d_gu, wgu[k], s_gu[k], W.EPI_SILU_MUL, None, None, hb)
         ctx.qmatmul_ex(d_d, wd[k], s_d[k], hb, None, W.EPI_ADD_RESIDUAL, None, x, xn)
 
     n = max(3, min(steps, 60))
     per = timed_graph(torch, ctx, launch, n, max(1, warmup // 4)) / n
-    for b in wgu + s_gu + wd + s_d + [x, gamma, nb, hb, xn]:
+    for b in wgu + s_gu + wd + s_d + [x, gamma, hb, xn]:
         b.free()
     gbs = ffn_bytes() / per / 1e9
     return {"us_per_step": round(per * 1e6, 2), "value": round(gbs, 2), "unit": "GB/s",
@@ -708,7 +708,7 @@ def main():
         log("bench: fp16 GEMV, 14336 x 4096")
         gh = bench_gemv_f16(torch, W, ctx, args.steps, args.warmup)
         log(f"  gemv_f16 {gh['us_per_launch']} us/launch, {gh['value']} GB/s")
-        log("bench: decode FFN step (rms_norm, gate/up + SILU_MUL, down + residual)")
+        log("bench: decode FFN step (rms_norm fused into gate/up + SILU_MUL, down + residual)")
         ff = bench_ffn(torch, W, ctx, args.steps, args.warmup)
         log(f"  decode FFN step {ff['us_per_step']} us/step, {ff['value']} GB/s")
         log("bench: fp32 GEMM through op_matmul_f32, 1024^3 and 4096^3")

@@ -30,7 +30,7 @@
 extern "C" {
 #endif
 
-#define LUX_HIP_QUANT_API_VERSION 4u
+#define LUX_HIP_QUANT_API_VERSION 5u
 
 /* Element types.  The first four keep LuxDtype's numbering (docs/api.md:188-197). */
 typedef enum LuxHipDtype {
@@ -265,6 +265,28 @@ typedef struct LuxHipRmsNormParams {
 LuxBackendError lux_hip_rms_norm(LuxBackendContext* ctx, const LuxHipRmsNormParams* params,
                                  LuxBackendBuffer* input, LuxBackendBuffer* gamma,
                                  LuxBackendBuffer* output, LuxBackendBuffer* rms_out);
+
+/* rms_norm followed by the quantized matmul, as one call: the composition of
+ * rms_norm (rms_norm.wgsl:50-110) and lux_hip_qmatmul_ex (matmul_nax_grouped,
+ * quantized_nax.wgsl:568-626, for the int4 GEMV); the reference has the two shaders and
+ * no fused form.  Rows r < desc->m of x [m x k] (norm->x_dtype) are normalised as
+ * lux_hip_rms_norm does, xn = x * r * gamma rounded to desc->x_dtype, and
+ * y = lux_hip_qmatmul_ex(desc, w, w_scales, xn, NULL, epilogue, bias, residual).
+ * norm->batch_size must equal desc->m, norm->hidden_size desc->k, norm->y_dtype
+ * desc->x_dtype (F32, F16 or BF16; x_scales are not taken, so W4A8 only with
+ * QUANTIZE_X).  The result is bit-identical to lux_hip_rms_norm into a buffer of
+ * desc->x_dtype followed by lux_hip_qmatmul_ex.  At m == 1 with int4 weights, SCALE_F16,
+ * x_dtype F16, flags 0 and k <= 8192 on the GEMV's fast path (k % 32 == 0, group_size a
+ * power-of-two multiple of 32 with an even number of groups per row), the GEMV computes
+ * the normalisation in its prologue (one launch; a decode step's rms_norm kernel and
+ * its output round trip disappear).  Other descriptors run rms_norm and then the
+ * matmul, with xn in the context workspace.  Errors as lux_hip_rms_norm and
+ * lux_hip_qmatmul_ex. */
+LuxBackendError lux_hip_rms_norm_qmatmul(LuxBackendContext* ctx, const LuxHipRmsNormParams* norm,
+                                         LuxBackendBuffer* gamma, const LuxHipQMatmulDesc* desc,
+                                         LuxBackendBuffer* w, LuxBackendBuffer* w_scales,
+                                         LuxBackendBuffer* x, int epilogue, LuxBackendBuffer* bias,
+                                         LuxBackendBuffer* residual, LuxBackendBuffer* y);
 
 /* GemvParams of gemv.wgsl:21-30. */
 typedef struct LuxHipGemvParams {

@@ -59,7 +59,7 @@ def test_null_arguments_rejected():
     assert L.lux_hip_context_set_synchronous(None, 1) == W.LUX_BACKEND_ERROR_INVALID_ARGUMENT
     assert L.lux_hip_buffer_wrap(None, None, 0) is None
     assert L.lux_hip_buffer_device_ptr(None) is None
-    assert L.lux_hip_quant_api_version() == 4
+    assert L.lux_hip_quant_api_version() == 5
     assert "NULL" in p.last_error() or p.last_error() != ""
 
 

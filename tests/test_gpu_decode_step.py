@@ -106,3 +106,121 @@ def test_decode_step_end_to_end(ctx):
     # the FFN branch on its own (the residual would hide errors in it)
     compare(ctx.download(db, np.float32, (1, hidden)).astype(np.float64), d.astype(np.float64),
             "decode step FFN branch")
+
+
+# ---- lux_hip_rms_norm_qmatmul: rms_norm fused ahead of the quantized matmul -------------
+CODES = {"f32": W.F32, "f16": W.F16, "bf16": W.BF16}
+YNP = {W.F32: np.float32, W.F16: np.float16, W.BF16: np.uint16}
+
+
+def _norm_input(r, m, k, xdt):
+    x = (r.standard_normal((m, k)) * 2).astype(np.float32)
+    if xdt == "f16":
+        return x.astype(np.float16)
+    if xdt == "bf16":
+        return bf16_bits(x)
+    return x
+
+
+def _fused_vs_two_calls(ctx, r, desc, xin, xdt, wp, s, epi, ydt, coding_bias=False):
+    """Run lux_hip_rms_norm_qmatmul and lux_hip_rms_norm + lux_hip_qmatmul_ex on the same
+    inputs; return both outputs as raw bits (they must be identical) and the normalised row."""
+    m, k, n_out = desc.m, desc.k, desc.n_out
+    ny = n_out // 2 if epi == W.EPI_SILU_MUL else n_out
+    gamma = r.uniform(0.5, 1.5, k).astype(np.float32)
+    bias = r.standard_normal(ny).astype(np.float32)
+    resid = r.standard_normal((m, ny)).astype(np.float32)
+    xb, gb, wb = ctx.upload(xin), ctx.upload(gamma), ctx.upload(wp)
+    sb = ctx.upload(s) if s is not None else None
+    bb = ctx.upload(bias) if epi == W.EPI_ADD_BIAS else None
+    rb = ctx.upload(resid) if epi == W.EPI_ADD_RESIDUAL else None
+    ynp = YNP[ydt]
+    y1, y2 = ctx.alloc(m * ny * np.dtype(ynp).itemsize), ctx.alloc(m * ny * np.dtype(ynp).itemsize)
+    nb = ctx.alloc(m * k * np.dtype(YNP[desc.x_dtype]).itemsize)
+    ctx.rms_norm_qmatmul(xb, gb, 1e-6, CODES[xdt], desc, wb, sb, epi, bb, rb, y1)
+    ctx.rms_norm(xb, gb, nb, m, k, 1e-6, CODES[xdt], desc.x_dtype)
+    ctx.qmatmul_ex(desc, wb, sb, nb, None, epi, bb, rb, y2)
+    got1 = ctx.download(y1, ynp, (m, ny))
+    got2 = ctx.download(y2, ynp, (m, ny))
+    return got1, got2, gamma
+
+
+@pytest.mark.parametrize("k,xdt,epi,ydt,coding", [
+    (4096, "f32", W.EPI_SILU_MUL, W.F16, 0),      # the decode FFN's gate/up call
+    (4096, "f16", W.EPI_NONE, W.F32, 0),
+    (4096, "bf16", W.EPI_ADD_BIAS, W.BF16, 1),
+    (2048, "f32", W.EPI_ADD_RESIDUAL, W.F32, 0),  # one slice per lane
+    (8192, "f32", W.EPI_SILU_MUL, W.F16, 1),      # four slices per lane: the largest fused k
+    (4128, "f16", W.EPI_NONE, W.F16, 0),          # k not a multiple of 256: ragged last pass
+    (96, "f32", W.EPI_NONE, W.F32, 0)])           # fewer elements than threads
+def test_rms_norm_qmatmul_fused_gemv_bit_identical(ctx, k, xdt, epi, ydt, coding):
+    """m = 1, int4, fp16 scales, fp16 activations: the GEMV normalises the row in its prologue.
+    The output must equal rms_norm followed by qmatmul_ex bit for bit, and the oracle."""
+    r = rng(k * 7 + len(xdt) + epi)
+    n_out, gs = 1030, 32
+    _, Wp, s = int4_weights(r, n_out, k, gs, coding)
+    xin = _norm_input(r, 1, k, xdt)
+    desc = W.qdesc(n_out, k, 1, 4, gs, coding, W.SCALE_F16, W.F16, ydt)
+    got1, got2, gamma = _fused_vs_two_calls(ctx, r, desc, xin, xdt, Wp, s, epi, ydt)
+    assert np.array_equal(got1.view(np.uint8), got2.view(np.uint8))
+    if epi == W.EPI_NONE:  # and the oracle on the plain GEMV
+        xf = xin.astype(np.float32) if xdt != "bf16" else bf16_to_f32(xin)
+        n, _ = oracle.rms_norm(xf, gamma, 1e-6)
+        n16 = n.astype(np.float16).astype(np.float32)
+        ref = oracle.qmatmul_f64(Wp, s.astype(np.float32), n16, gs, 4)
+        got = bf16_to_f32(got1) if ydt == W.BF16 else got1.astype(np.float32)
+        yname = {W.F32: "f32", W.F16: "f16", W.BF16: "bf16"}[ydt]
+        compare(got.astype(np.float64), round_to(ref.astype(np.float32), yname), f"rms_norm_qmatmul k{k}")
+
+
+@pytest.mark.parametrize("case", ["small_m", "k16384", "scale_f32", "x_f32", "w8", "w4a8_qx"])
+def test_rms_norm_qmatmul_two_launch_routes(ctx, case):
+    """Descriptors outside the fused GEMV run rms_norm into the workspace, then the matmul:
+    still bit-identical to the two separate calls."""
+    r = rng(len(case) * 31)
+    m, n_out, k, bits, gs, sf, xdt, ydt, flags, epi = 1, 512, 4096, 4, 32, W.SCALE_F16, W.F16, W.F16, 0, W.EPI_NONE
+    if case == "small_m":
+        m, epi = 5, W.EPI_SILU_MUL
+    elif case == "k16384":
+        k = 16384
+    elif case == "scale_f32":
+        sf = W.SCALE_F32
+    elif case == "x_f32":
+        xdt, ydt = W.F32, W.F32
+    elif case == "w8":
+        bits, m, gs = 8, 3, k  # per-row int8 scales (config 3's format)
+    elif case == "w4a8_qx":
+        m, gs, flags, ydt, xdt = 33, 128, W.QFLAG_QUANTIZE_X, W.F32, W.F32
+    if bits == 4:
+        _, Wp, s = int4_weights(r, n_out, k, gs)
+    else:
+        q = r.integers(-127, 128, size=(n_out, k)).astype(np.int8)
+        Wp, s = q, r.uniform(0.001, 0.01, size=(n_out, k // gs)).astype(np.float16)
+    if sf == W.SCALE_F32:
+        s = s.astype(np.float32)
+    desc = W.qdesc(n_out, k, m, bits, gs, 0, sf, xdt, ydt)
+    desc.flags = flags
+    xin = _norm_input(r, m, k, "f32")
+    got1, got2, _ = _fused_vs_two_calls(ctx, r, desc, xin, "f32", Wp, s, epi, ydt)
+    assert np.array_equal(got1.view(np.uint8), got2.view(np.uint8))
+
+
+def test_rms_norm_qmatmul_rejects(ctx):
+    r = rng(5)
+    k, n_out = 256, 64
+    _, Wp, s = int4_weights(r, n_out, k, 32)
+    xb, gb, wb, sb = ctx.upload(np.ones(k, np.float32)), ctx.upload(np.ones(k, np.float32)), ctx.upload(Wp), ctx.upload(s)
+    yb = ctx.alloc(n_out * 2)
+    d = W.qdesc(n_out, k, 1, 4, 32, 0, W.SCALE_F16, W.F16, W.F16)
+    lib = ctx.plugin.lib
+
+    def call(p, desc, gamma=gb):
+        return lib.lux_hip_rms_norm_qmatmul(ctx.handle, W.byref(p), gamma.handle, W.byref(desc), wb.handle,
+                                            sb.handle, xb.handle, W.EPI_NONE, None, None, yb.handle)
+    assert call(W.RmsNormParams(1, k, 1e-6, W.F32, W.F16), d) == W.LUX_BACKEND_OK
+    assert call(W.RmsNormParams(2, k, 1e-6, W.F32, W.F16), d) == W.LUX_BACKEND_ERROR_INVALID_ARGUMENT  # m
+    assert call(W.RmsNormParams(1, k - 32, 1e-6, W.F32, W.F16), d) == W.LUX_BACKEND_ERROR_INVALID_ARGUMENT  # k
+    assert call(W.RmsNormParams(1, k, 1e-6, W.F32, W.F32), d) == W.LUX_BACKEND_ERROR_INVALID_ARGUMENT  # y != x dtype
+    assert call(W.RmsNormParams(1, k, 1e-6, W.I8, W.F16), d) == W.LUX_BACKEND_ERROR_NOT_SUPPORTED
+    small = ctx.upload(np.ones(k // 2, np.float32))
+    assert call(W.RmsNormParams(1, k, 1e-6, W.F32, W.F16), d, small) == W.LUX_BACKEND_ERROR_INVALID_ARGUMENT

@@ -152,6 +152,9 @@ EXPORTS = {
                                         c_void_p, c_int, c_void_p, c_void_p, c_void_p]),
     "lux_hip_rms_norm": (c_int, [c_void_p, POINTER(RmsNormParams), c_void_p, c_void_p, c_void_p,
                                  c_void_p]),
+    "lux_hip_rms_norm_qmatmul": (c_int, [c_void_p, POINTER(RmsNormParams), c_void_p,
+                                         POINTER(QMatmulDesc), c_void_p, c_void_p, c_void_p, c_int,
+                                         c_void_p, c_void_p, c_void_p]),
     "lux_hip_quantize": (c_int, [c_void_p, POINTER(QuantizeDesc), c_void_p, c_void_p, c_void_p]),
     "lux_hip_dequantize": (c_int, [c_void_p, POINTER(QuantizeDesc), c_void_p, c_void_p, c_void_p]),
     "lux_hip_convert_nibbles": (c_int, [c_void_p, c_void_p, c_void_p, c_size_t, c_int, c_int]),
@@ -425,6 +428,17 @@ class Context:
         self.plugin.check(self.lib.lux_hip_rms_norm(self.handle, byref(p), x.handle, gamma.handle,
                                                     y.handle, rms_out.handle if rms_out else None),
                           "rms_norm")
+
+    def rms_norm_qmatmul(self, x: Buffer, gamma: Buffer, eps: float, x_dtype: int,
+                         desc: QMatmulDesc, w: Buffer, scales: Buffer | None, epilogue: int,
+                         bias: Buffer | None, residual: Buffer | None, y: Buffer):
+        """lux_hip_rms_norm_qmatmul: rms_norm of x ([desc.m x desc.k], x_dtype) into
+        desc.x_dtype, then lux_hip_qmatmul_ex on the normalised rows."""
+        p = RmsNormParams(desc.m, desc.k, eps, x_dtype, desc.x_dtype)
+        self.plugin.check(self.lib.lux_hip_rms_norm_qmatmul(
+            self.handle, byref(p), gamma.handle, byref(desc), w.handle,
+            scales.handle if scales else None, x.handle, epilogue, bias.handle if bias else None,
+            residual.handle if residual else None, y.handle), "rms_norm_qmatmul")
 
     def quantize(self, desc: QuantizeDesc, x: Buffer, q: Buffer, scales: Buffer):
         self.plugin.check(self.lib.lux_hip_quantize(self.handle, byref(desc), x.handle, q.handle,

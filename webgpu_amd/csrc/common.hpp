@@ -40,6 +40,15 @@ struct EpiArgs {
 enum class XKind : int { F32 = 0, F16 = 1, BF16 = 2, I8 = 32 };
 enum class YKind : int { F32 = 0, F16 = 1, BF16 = 2, I32 = 3 };
 
+// rms_norm of the GEMV's activation row computed in the GEMV's own prologue
+// (rms_norm.wgsl:50-110 fused ahead of the int4 GEMV).
+struct RnArgs {
+    const void* x;       // the row before normalisation, XKind xk
+    const float* gamma;  // [k]
+    float eps;
+    int xk;              // XKind::F32, F16 or BF16
+};
+
 #if defined(__HIP_DEVICE_COMPILE__) || defined(__HIPCC__)
 __device__ __forceinline__ float load_scale(const void* s, size_t idx, ScaleKind kind) {
     switch (kind) {
@@ -272,6 +281,8 @@ struct QArgs {
     bool group_partials;  // W4A8: write P[m][n][g]
     EpiArgs epi;          // output epilogue; SiluMul: n_out = 2 * (output columns),
                           // weight rows [0, n_out/2) gate and [n_out/2, n_out) up
+    RnArgs rn;            // rn.gamma != null: x is rms_norm(rn.x) rounded to fp16, computed by the
+                          // GEMV itself (m = 1 int4 fast path only; a.x is unused)
 };
 
 hipError_t launch_gemv_f32(const float* A, const float* x, float* y, int M, int K, int lda,
@@ -291,6 +302,8 @@ hipError_t launch_gemv_f16(const void* A, const void* x, float* y, int M, int K,
 // int4 weight-only GEMV, m == 1.
 bool qgemv_i4_fast(const QArgs& a);  // the m = 1 int4 GEMV fast path applies (SiluMul needs it)
 hipError_t launch_qgemv_i4(const QArgs& a, hipStream_t s);
+// The GEMV can normalise its own activation row (a.rn): m = 1, int4, fp16 scales, k <= 8192.
+bool qgemv_i4_rn_supported(const QArgs& a);
 // Per-weight-row scale folds (scale_fold_factor) of int4 weights staged as fp16:
 // fold[n] for n < n_out, one wave per row.
 hipError_t launch_scale_fold(const void* s, ScaleKind sk, int n_out, int groups, float* fold, hipStream_t st);

@@ -594,10 +594,15 @@ LUX_EXPORT LuxBackendError lux_hip_gemv_f16(LuxBackendContext* ctx, LuxBackendBu
 namespace {
 // noalloc: staging buffers come from the device's fixed `scratch` array (at most
 // kScratchBytes) instead of the context workspace; nothing is allocated.
+// ws_offset: the first ws_offset bytes of the context workspace hold a caller's data
+// (rms_norm_qmatmul's normalised rows) and are left alone.
+// rn: x is the row before rms_norm, normalised by the GEMV itself (the caller checked
+// qgemv_i4_rn_supported; x_dtype F16 names the normalised row's type).
 LuxBackendError qmatmul_impl(LuxBackendContext* ctx, const LuxHipQMatmulDesc* d, LuxBackendBuffer* w,
                              LuxBackendBuffer* w_scales, LuxBackendBuffer* x, LuxBackendBuffer* x_scales,
                              int epilogue, LuxBackendBuffer* bias, LuxBackendBuffer* residual,
-                             LuxBackendBuffer* y, bool noalloc = false) {
+                             LuxBackendBuffer* y, bool noalloc = false, size_t ws_offset = 0,
+                             const RnArgs* rn = nullptr) {
     HipCtx* c = C(ctx);
     if (!c || !d || !w || !x || !y) return fail(LUX_BACKEND_ERROR_INVALID_ARGUMENT, "qmatmul: NULL argument");
     if (epilogue < LUX_HIP_EPILOGUE_NONE || epilogue > LUX_HIP_EPILOGUE_SILU_MUL)
@@ -669,7 +674,12 @@ LuxBackendError qmatmul_impl(LuxBackendContext* ctx, const LuxHipQMatmulDesc* d,
     if (LuxBackendError e = begin_op(c, "qmatmul")) return e;
     if (M == 0 || n_out == 0) return LUX_BACKEND_OK;
     auto workspace = [&](size_t bytes, void** out) -> LuxBackendError {
-        if (!noalloc) return get_workspace(c, bytes, out, "qmatmul");
+        if (!noalloc) {
+            void* base = nullptr;
+            if (LuxBackendError e = get_workspace(c, ws_offset + bytes, &base, "qmatmul")) return e;
+            *out = static_cast<unsigned char*>(base) + ws_offset;
+            return LUX_BACKEND_OK;
+        }
         if (bytes > kScratchBytes)
             return fail(LUX_BACKEND_ERROR_NOT_SUPPORTED,
                         "qmatmul_noalloc: this shape needs %zu bytes of scratch, above the maximum of %zu", bytes,
@@ -700,7 +710,12 @@ LuxBackendError qmatmul_impl(LuxBackendContext* ctx, const LuxHipQMatmulDesc* d,
     a.xor_mask = (d->weight_bits == 4 && d->nibble_coding == LUX_HIP_NIBBLE_TWOS_COMPLEMENT) ? 0x88888888u : 0u;
 
     hipError_t he;
-    if (w4a8) {
+    if (rn) {
+        a.rn = *rn;
+        if (w4a8 || !qgemv_i4_rn_supported(a))
+            return fail(LUX_BACKEND_ERROR_INTERNAL, "qmatmul: fused rms_norm on a path without it");
+        he = launch_qgemv_i4(a, c->stream);
+    } else if (w4a8) {
         if (qx) {  // int8 activations and their f32 per-token scales in the workspace
             a.x_kind = XKind::I8;
             void* wsv = nullptr;
@@ -929,6 +944,74 @@ LUX_EXPORT LuxBackendError lux_hip_rms_norm(LuxBackendContext* ctx, const LuxHip
                                      static_cast<YKind>(p->y_dtype), R ? static_cast<float*>(R->ptr) : nullptr,
                                      (int)p->batch_size, (int)p->hidden_size, p->eps, c->stream),
                   "rms_norm");
+}
+
+// rms_norm (rms_norm.wgsl:50-110) of X into desc->x_dtype, then the quantized matmul of
+// lux_hip_qmatmul_ex on the normalised rows.  At m == 1 with int4 weights, fp16 scales and
+// an fp16 activation type, the GEMV normalises the row in its own prologue: one launch and
+// no intermediate row in memory.  Otherwise the two kernels run back to back with the
+// normalised rows at the start of the context workspace.  Both routes give the bits of
+// lux_hip_rms_norm followed by lux_hip_qmatmul_ex.
+LUX_EXPORT LuxBackendError lux_hip_rms_norm_qmatmul(LuxBackendContext* ctx, const LuxHipRmsNormParams* p,
+                                                    LuxBackendBuffer* gamma, const LuxHipQMatmulDesc* d,
+                                                    LuxBackendBuffer* w, LuxBackendBuffer* w_scales,
+                                                    LuxBackendBuffer* x, int epilogue, LuxBackendBuffer* bias,
+                                                    LuxBackendBuffer* residual, LuxBackendBuffer* y) {
+    HipCtx* c = C(ctx);
+    HipBuf *X = B(x), *G = B(gamma), *W = B(w), *S = B(w_scales);
+    if (!c || !p || !d || !X || !G || !W || !y)
+        return fail(LUX_BACKEND_ERROR_INVALID_ARGUMENT, "rms_norm_qmatmul: NULL argument");
+    if (d->struct_size < sizeof(LuxHipQMatmulDesc))
+        return fail(LUX_BACKEND_ERROR_INVALID_ARGUMENT, "rms_norm_qmatmul: struct_size %u too small", d->struct_size);
+    auto fp = [](int t) { return t == LUX_HIP_F32 || t == LUX_HIP_F16 || t == LUX_HIP_BF16; };
+    if (!fp(p->x_dtype) || !fp(d->x_dtype))
+        return fail(LUX_BACKEND_ERROR_NOT_SUPPORTED,
+                    "rms_norm_qmatmul: x and the normalised rows must be F32, F16 or BF16");
+    if (p->y_dtype != d->x_dtype)
+        return fail(LUX_BACKEND_ERROR_INVALID_ARGUMENT,
+                    "rms_norm_qmatmul: the norm's y_dtype must equal the matmul's x_dtype");
+    if (d->m < 0 || d->k < 0 || (int64_t)p->batch_size != d->m || (int64_t)p->hidden_size != d->k)
+        return fail(LUX_BACKEND_ERROR_INVALID_ARGUMENT,
+                    "rms_norm_qmatmul: batch_size and hidden_size must equal the matmul's m and k");
+    if (d->k == 0 && d->m != 0) return fail(LUX_BACKEND_ERROR_INVALID_ARGUMENT, "rms_norm_qmatmul: hidden_size 0");
+    const size_t xb = dtype_bytes(p->x_dtype), n = (size_t)d->m * d->k;
+    if (!fits(X, n * xb) || !fits(G, (size_t)d->k * 4))
+        return fail(LUX_BACKEND_ERROR_INVALID_ARGUMENT, "rms_norm_qmatmul: x or gamma buffer too small");
+    if (((uintptr_t)X->ptr & (xb - 1)) || ((uintptr_t)G->ptr & 3u))
+        return fail(LUX_BACKEND_ERROR_NOT_SUPPORTED, "rms_norm_qmatmul: x or gamma not naturally aligned");
+    const RnArgs rn{X->ptr, static_cast<const float*>(G->ptr), p->eps, p->x_dtype};
+
+    QArgs probe{};
+    probe.w = W->ptr;
+    probe.s = S ? S->ptr : nullptr;
+    probe.n_out = d->n_out;
+    probe.k = d->k;
+    probe.m = d->m;
+    probe.group_size = d->group_size;
+    probe.wbits = d->weight_bits;
+    probe.scale_kind = static_cast<ScaleKind>(d->scale_format);
+    probe.x_kind = static_cast<XKind>(d->x_dtype);
+    probe.rn = rn;
+    if (d->flags == 0 && S && d->n_out > 0 && d->x_dtype == LUX_HIP_F16 && d->scale_format == LUX_HIP_SCALE_F16 &&
+        qgemv_i4_rn_supported(probe))
+        return qmatmul_impl(ctx, d, w, w_scales, x, nullptr, epilogue, bias, residual, y, false, 0, &rn);
+
+    if (LuxBackendError e = begin_op(c, "rms_norm_qmatmul")) return e;
+    HipBuf xn;
+    xn.size = (n * dtype_bytes(d->x_dtype) + 255) & ~(size_t)255;
+    xn.owned = false;
+    xn.device = c->device;
+    if (n) {
+        if (LuxBackendError e = get_workspace(c, xn.size, &xn.ptr, "rms_norm_qmatmul")) return e;
+        if (hipError_t he = launch_rms_norm(X->ptr, static_cast<XKind>(p->x_dtype), rn.gamma, xn.ptr,
+                                            static_cast<YKind>(d->x_dtype), nullptr, d->m, d->k, p->eps, c->stream);
+            he != hipSuccess)
+            return end_op(c, he, "rms_norm_qmatmul (rms_norm)");
+    } else {
+        xn.ptr = X->ptr;  // nothing to normalise; the matmul validates and returns
+    }
+    return qmatmul_impl(ctx, d, w, w_scales, reinterpret_cast<LuxBackendBuffer*>(&xn), nullptr, epilogue, bias,
+                        residual, y, false, xn.size);
 }
 
 // quantize_int8_per_channel / dequantize_int8_per_channel (quantized.wgsl:264-297):

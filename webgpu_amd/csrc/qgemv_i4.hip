@@ -18,6 +18,9 @@
 //   - x is read once per block and shared through LDS;
 //   - each wave owns a run of rows and keeps two rows of loads in flight ahead of
 //     its math; the row sums use a VALU-only DPP wave reduction.
+// lux_hip_rms_norm_qmatmul instantiates the same kernel with RN: every block normalises
+// the activation row itself (rms_norm.wgsl:50-110, k_rms_norm's arithmetic and order)
+// while its first weight rows are in flight, so a decode step needs no rms_norm launch.
 #include <cstdlib>
 
 #include "common.hpp"
@@ -54,12 +57,16 @@ __device__ __forceinline__ float dot_slice_sub(const uint32_t (&q)[4], const f16
 // SM (SiluMul epilogue): the wave's rows are read as interleaved pairs, gate row g then
 // up row n_out/2 + g (virtual row v -> v even: v/2, v odd: n_out/2 + v/2; RW is even, so a
 // pair never straddles two waves), and lane 2p stores silu(gate) * up to y[g].
-template <int SPL, int RW, int D, ScaleKind SK, YKind YK, bool XOR, bool SM>
+// RN: x is not read; the block computes x = fp16(rn.x * r * gamma), r = 1 / sqrt(sum(rn.x^2)
+// / K + eps), with k_rms_norm's arithmetic in k_rms_norm's order (thread t sums elements
+// t + 256 j, j ascending, then the DPP wave sum and the four wave sums in a fixed order),
+// so the staged row is bit-identical to what k_rms_norm would have written.
+template <int SPL, int RW, int D, ScaleKind SK, YKind YK, bool XOR, bool SM, bool RN>
 __global__ __launch_bounds__(256) void k_qgemv_i4_f16(const u32x4* __restrict__ W,
                                                       const void* __restrict__ S,
                                                       const f16* __restrict__ x,
                                                       void* __restrict__ y, int n_out, int K,
-                                                      int spg_shift, uint32_t xor_mask, EpiArgs epi) {
+                                                      int spg_shift, uint32_t xor_mask, EpiArgs epi, RnArgs rn) {
     __shared__ u32x4 xs[SPL * 256];  // K <= SPL * 2048 halves
     const int lane = threadIdx.x & 63;
     const int row0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * RW;
@@ -73,10 +80,28 @@ __global__ __launch_bounds__(256) void k_qgemv_i4_f16(const u32x4* __restrict__ 
     // addresses are clamped to valid ones; out-of-range slices get x = 0 after the
     // loads, and rows past the wave's share are never computed or stored.
     u32x4 xv[SPL];
+    constexpr int NJ = RN ? 8 * SPL : 1;  // RN: row elements per thread (K <= 2048 * SPL)
+    float xe[NJ], ge[NJ];
+    if constexpr (RN) {
+        const int last = K - 1;
+        if (rn.xk == (int)XKind::F32) {
 #pragma unroll
-    for (int j = 0; j < SPL; ++j) {
-        const int c = threadIdx.x + 256 * j;
-        xv[j] = c < K / 8 ? reinterpret_cast<const u32x4*>(x)[c] : u32x4{0u, 0u, 0u, 0u};
+            for (int j = 0; j < NJ; ++j) xe[j] = load_x<XKind::F32>(rn.x, min((int)threadIdx.x + 256 * j, last));
+        } else if (rn.xk == (int)XKind::F16) {
+#pragma unroll
+            for (int j = 0; j < NJ; ++j) xe[j] = load_x<XKind::F16>(rn.x, min((int)threadIdx.x + 256 * j, last));
+        } else {
+#pragma unroll
+            for (int j = 0; j < NJ; ++j) xe[j] = load_x<XKind::BF16>(rn.x, min((int)threadIdx.x + 256 * j, last));
+        }
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) ge[j] = rn.gamma[min((int)threadIdx.x + 256 * j, last)];
+    } else {
+#pragma unroll
+        for (int j = 0; j < SPL; ++j) {
+            const int c = threadIdx.x + 256 * j;
+            xv[j] = c < K / 8 ? reinterpret_cast<const u32x4*>(x)[c] : u32x4{0u, 0u, 0u, 0u};
+        }
     }
     __builtin_amdgcn_sched_barrier(0);  // keep x loads ahead of the weight stream
     int sl[SPL];
@@ -103,10 +128,31 @@ __global__ __launch_bounds__(256) void k_qgemv_i4_f16(const u32x4* __restrict__ 
 #pragma unroll
     for (int r = 0; r < (D < RW ? D : RW); ++r) issue(r);
     __builtin_amdgcn_sched_barrier(0);
+    if constexpr (RN) {
+        __shared__ float part[4];
+        float ss = 0.0f;
 #pragma unroll
-    for (int j = 0; j < SPL; ++j) {
-        const int c = threadIdx.x + 256 * j;
-        if (c < K / 8) xs[c] = xv[j];
+        for (int j = 0; j < NJ; ++j) {
+            const float v = (int)threadIdx.x + 256 * j < K ? xe[j] : 0.0f;
+            ss = fmaf(v, v, ss);
+        }
+        ss = wave_sum(ss);
+        if (lane == 0) part[threadIdx.x >> 6] = ss;
+        __syncthreads();
+        const float mean_sq = ((part[0] + part[1]) + (part[2] + part[3])) / (float)K;
+        const float r = 1.0f / sqrtf(mean_sq + rn.eps);
+        f16* xh = reinterpret_cast<f16*>(xs);
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) {
+            const int i = threadIdx.x + 256 * j;
+            if (i < K) xh[i] = (f16)(xe[j] * r * ge[j]);  // RNE, as k_rms_norm's fp16 store
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < SPL; ++j) {
+            const int c = threadIdx.x + 256 * j;
+            if (c < K / 8) xs[c] = xv[j];
+        }
     }
     __syncthreads();  // every wave of the block reaches this before any returns
     if (!active) return;
@@ -189,7 +235,7 @@ __global__ __launch_bounds__(256) void k_qgemv_i4_generic(const uint32_t* __rest
     if (lane == 0) store_y<YK>(y, row, apply_epi(acc, epi, 0, row, n_out));
 }
 
-template <int SPL, int RW, int D, ScaleKind SK, YKind YK>
+template <int SPL, int RW, int D, ScaleKind SK, YKind YK, bool RN>
 static void launch_rwd(const QArgs& a, hipStream_t s) {
     const int waves = (a.n_out + RW - 1) / RW;
     const dim3 grid((waves + 3) / 4), block(256);
@@ -197,32 +243,32 @@ static void launch_rwd(const QArgs& a, hipStream_t s) {
     const f16* x = reinterpret_cast<const f16*>(a.x);
     const int shift = __builtin_ctz(a.group_size / 32);
     auto go = [&](auto kern) {
-        hipLaunchKernelGGL(kern, grid, block, 0, s, w, a.s, x, a.y, a.n_out, a.k, shift, a.xor_mask, a.epi);
+        hipLaunchKernelGGL(kern, grid, block, 0, s, w, a.s, x, a.y, a.n_out, a.k, shift, a.xor_mask, a.epi, a.rn);
     };
     const bool sm = a.epi.kind == (int)Epi::SiluMul;
     if constexpr (RW % 2 == 0) {
         if (sm) {
-            if (a.xor_mask) go(k_qgemv_i4_f16<SPL, RW, D, SK, YK, true, true>);
-            else go(k_qgemv_i4_f16<SPL, RW, D, SK, YK, false, true>);
+            if (a.xor_mask) go(k_qgemv_i4_f16<SPL, RW, D, SK, YK, true, true, RN>);
+            else go(k_qgemv_i4_f16<SPL, RW, D, SK, YK, false, true, RN>);
             return;
         }
     }
-    if (a.xor_mask) go(k_qgemv_i4_f16<SPL, RW, D, SK, YK, true, false>);
-    else go(k_qgemv_i4_f16<SPL, RW, D, SK, YK, false, false>);
+    if (a.xor_mask) go(k_qgemv_i4_f16<SPL, RW, D, SK, YK, true, false, RN>);
+    else go(k_qgemv_i4_f16<SPL, RW, D, SK, YK, false, false, RN>);
 }
 
 // Two rows of prefetch (issue row r+2, then compute row r) measured best on MI355X for
 // config 2 (6.9 us against 7.0 us with one row); issuing all rows up front bunches the
 // arrivals and lengthens the tail (8.6 us).
-template <int SPL, int RW, ScaleKind SK, YKind YK>
+template <int SPL, int RW, ScaleKind SK, YKind YK, bool RN>
 static void launch_rw(const QArgs& a, hipStream_t s) {
-    launch_rwd<SPL, RW, 2, SK, YK>(a, s);
+    launch_rwd<SPL, RW, 2, SK, YK, RN>(a, s);
 }
 
 // Rows per wave: enough for 8 waves per CU with equal shares (14336 rows on 256
 // CUs -> 7 rows per wave, 2048 waves); capped so the weight registers
 // (RW * SPL * 4 VGPRs) stay within 64.
-template <int SPL, ScaleKind SK, YKind YK>
+template <int SPL, ScaleKind SK, YKind YK, bool RN>
 static void launch_fast(const QArgs& a, hipStream_t s) {
     constexpr int RWMAX = SPL <= 2 ? 8 : 16 / SPL;
     const int target_waves = device_cus() * 8;
@@ -230,35 +276,41 @@ static void launch_fast(const QArgs& a, hipStream_t s) {
     rw = rw < 1 ? 1 : (rw > RWMAX ? RWMAX : rw);
     if (a.epi.kind == (int)Epi::SiluMul) rw += rw & 1;  // whole gate/up pairs per wave (RWMAX is even)
     switch (rw) {
-        case 1: launch_rw<SPL, 1, SK, YK>(a, s); break;
-        case 2: launch_rw<SPL, 2, SK, YK>(a, s); break;
-        case 3: if constexpr (RWMAX >= 3) launch_rw<SPL, 3, SK, YK>(a, s); break;
-        case 4: if constexpr (RWMAX >= 4) launch_rw<SPL, 4, SK, YK>(a, s); break;
-        case 5: if constexpr (RWMAX >= 5) launch_rw<SPL, 5, SK, YK>(a, s); break;
-        case 6: if constexpr (RWMAX >= 6) launch_rw<SPL, 6, SK, YK>(a, s); break;
-        case 7: if constexpr (RWMAX >= 7) launch_rw<SPL, 7, SK, YK>(a, s); break;
-        default: if constexpr (RWMAX >= 8) launch_rw<SPL, 8, SK, YK>(a, s); break;
+        case 1: launch_rw<SPL, 1, SK, YK, RN>(a, s); break;
+        case 2: launch_rw<SPL, 2, SK, YK, RN>(a, s); break;
+        case 3: if constexpr (RWMAX >= 3) launch_rw<SPL, 3, SK, YK, RN>(a, s); break;
+        case 4: if constexpr (RWMAX >= 4) launch_rw<SPL, 4, SK, YK, RN>(a, s); break;
+        case 5: if constexpr (RWMAX >= 5) launch_rw<SPL, 5, SK, YK, RN>(a, s); break;
+        case 6: if constexpr (RWMAX >= 6) launch_rw<SPL, 6, SK, YK, RN>(a, s); break;
+        case 7: if constexpr (RWMAX >= 7) launch_rw<SPL, 7, SK, YK, RN>(a, s); break;
+        default: if constexpr (RWMAX >= 8) launch_rw<SPL, 8, SK, YK, RN>(a, s); break;
     }
 }
 
-template <ScaleKind SK, YKind YK>
+// RN (the GEMV normalises its own row): one to four slices per lane (k <= 8192), so that
+// the row's elements and gamma stay in registers through the prologue (8 * SPL each).
+template <ScaleKind SK, YKind YK, bool RN>
 static bool dispatch_spl(const QArgs& a, hipStream_t s) {
     const int slices = a.k / 32;
     const int spl = (slices + 63) / 64;
-    if (spl <= 1) launch_fast<1, SK, YK>(a, s);
-    else if (spl <= 2) launch_fast<2, SK, YK>(a, s);
-    else if (spl <= 4) launch_fast<4, SK, YK>(a, s);
-    else if (spl <= 8) launch_fast<8, SK, YK>(a, s);
-    else return false;
+    if (spl <= 1) launch_fast<1, SK, YK, RN>(a, s);
+    else if (spl <= 2) launch_fast<2, SK, YK, RN>(a, s);
+    else if (spl <= 4) launch_fast<4, SK, YK, RN>(a, s);
+    else if constexpr (!RN) {
+        if (spl <= 8) launch_fast<8, SK, YK, RN>(a, s);
+        else return false;
+    } else {
+        return false;
+    }
     return true;
 }
 
-template <ScaleKind SK>
+template <ScaleKind SK, bool RN>
 static bool dispatch_y(const QArgs& a, hipStream_t s) {
     switch (a.y_kind) {
-        case YKind::F32: return dispatch_spl<SK, YKind::F32>(a, s);
-        case YKind::F16: return dispatch_spl<SK, YKind::F16>(a, s);
-        case YKind::BF16: return dispatch_spl<SK, YKind::BF16>(a, s);
+        case YKind::F32: return dispatch_spl<SK, YKind::F32, RN>(a, s);
+        case YKind::F16: return dispatch_spl<SK, YKind::F16, RN>(a, s);
+        case YKind::BF16: return dispatch_spl<SK, YKind::BF16, RN>(a, s);
         default: return false;
     }
 }
@@ -290,19 +342,30 @@ bool qgemv_i4_fast(const QArgs& a) {
     const int spg = a.group_size / 32;
     return a.x_kind == XKind::F16 && a.k % 32 == 0 && a.k <= 16384 && a.group_size % 32 == 0 && spg > 0 &&
            (spg & (spg - 1)) == 0 && (a.scale_kind != ScaleKind::F16 || (a.k / a.group_size) % 2 == 0) &&
-           a.scale_kind != ScaleKind::None && ((uintptr_t)a.w & 15u) == 0 && ((uintptr_t)a.x & 15u) == 0 &&
+           a.scale_kind != ScaleKind::None && ((uintptr_t)a.w & 15u) == 0 &&
+           (a.rn.gamma != nullptr || ((uintptr_t)a.x & 15u) == 0) &&
            ((uintptr_t)a.s & 3u) == 0;  // fp16 scales are read as aligned u32 pairs
 }
 
+bool qgemv_i4_rn_supported(const QArgs& a) {
+    QArgs b = a;
+    if (!b.rn.gamma) b.rn.gamma = reinterpret_cast<const float*>(16);  // only the x-alignment test differs
+    return a.m == 1 && a.wbits == 4 && a.scale_kind == ScaleKind::F16 && a.k <= 8192 && qgemv_i4_fast(b);
+}
+
 hipError_t launch_qgemv_i4(const QArgs& a, hipStream_t s) {
+    if (a.rn.gamma) {  // the caller checked qgemv_i4_rn_supported
+        if (!qgemv_i4_rn_supported(a) || !dispatch_y<ScaleKind::F16, true>(a, s)) return hipErrorInvalidValue;
+        return hipGetLastError();
+    }
     const bool fast = qgemv_i4_fast(a);
     if (a.epi.kind == (int)Epi::SiluMul && !fast) return hipErrorInvalidValue;  // the caller checks
     bool launched = false;
     if (fast) {
         switch (a.scale_kind) {
-            case ScaleKind::F16: launched = dispatch_y<ScaleKind::F16>(a, s); break;
-            case ScaleKind::F32: launched = dispatch_y<ScaleKind::F32>(a, s); break;
-            case ScaleKind::GroupScale: launched = dispatch_y<ScaleKind::GroupScale>(a, s); break;
+            case ScaleKind::F16: launched = dispatch_y<ScaleKind::F16, false>(a, s); break;
+            case ScaleKind::F32: launched = dispatch_y<ScaleKind::F32, false>(a, s); break;
+            case ScaleKind::GroupScale: launched = dispatch_y<ScaleKind::GroupScale, false>(a, s); break;
             default: break;
         }
     }

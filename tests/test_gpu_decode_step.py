@@ -95,6 +95,15 @@ def test_decode_step_end_to_end(ctx):
                 ctx.upload(Wd), ctx.upload(sd), hb, None, db)
     ctx.binary_f32("add", xb, db, outb, hidden)
     got = ctx.download(outb, np.float32, (1, hidden)).astype(np.float64)
+    # the same step in two launches (bench.py's form): rms_norm inside the gate/up GEMV,
+    # the residual in the down GEMV's epilogue; the same bits as the four calls
+    hb2, outb2 = ctx.alloc(inter * 2), ctx.alloc(hidden * 4)
+    ctx.rms_norm_qmatmul(xb, gb, 1e-6, W.F32, W.qdesc(2 * inter, hidden, 1, 4, gs, 0, W.SCALE_F16, W.F16, W.F16),
+                         ctx.upload(Wgu), ctx.upload(sgu), W.EPI_SILU_MUL, None, None, hb2)
+    ctx.qmatmul_ex(W.qdesc(hidden, inter, 1, 4, gs, 0, W.SCALE_F16, W.F16, W.F32),
+                   ctx.upload(Wd), ctx.upload(sd), hb2, None, W.EPI_ADD_RESIDUAL, None, xb, outb2)
+    assert np.array_equal(ctx.download(outb2, np.float32, (1, hidden)).view(np.uint32),
+                          got.astype(np.float32).view(np.uint32))
     # oracle composition, rounding to fp16 where the plugin stores fp16
     n, _ = oracle.rms_norm(x, gamma, 1e-6)
     n16 = n.astype(np.float16).astype(np.float32)

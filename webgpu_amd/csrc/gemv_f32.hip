@@ -214,33 +214,53 @@ __global__ __launch_bounds__(256) void k_gemv_t_partial(const float* __restrict_
     }
 }
 
-// Pass 2: a block takes 64 columns; wave w adds chunks w, w + 4, ... (loads issued 8 at a
-// time), and the four sums meet in LDS in wave order.  (One thread per column walking all
-// chunks took 19 us for 64 chunks x 4096 columns: one load round trip per chunk.)
+// Pass 2: a block takes 64 columns.  With N % 4 == 0 (VEC), 16 lanes cover the 64 columns
+// with 16-B loads and the block's 16 such groups take chunks g, g + 16, ... (at most 16
+// per thread for 256 chunks, issued 8 at a time), so one round trip covers 64 chunks;
+// otherwise lane = column and wave w takes chunks w, w + 4, ....  The group sums meet in
+// LDS and are added in group order.  (One thread per column walking all chunks took 19 us
+// for 64 chunks x 4096 columns: one load round trip per chunk.)
+template <bool VEC>
 __global__ __launch_bounds__(256) void k_gemv_t_reduce(const float* __restrict__ P, float* __restrict__ y, int N,
                                                        int C, float alpha, float beta) {
-    __shared__ float red[4][64];
-    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-    const int n = blockIdx.x * 64 + lane;
-    float s = 0.f;
+    constexpr int CPL = VEC ? 4 : 1, NG = VEC ? 16 : 4;  // columns per lane, chunk groups
+    __shared__ float red[NG][64];
+    const int tid = threadIdx.x;
+    const int cl = VEC ? (tid & 15) * 4 : (tid & 63);  // first column of the thread in the block
+    const int g = VEC ? tid >> 4 : tid >> 6;
+    const int n = blockIdx.x * 64 + cl;
+    float s[CPL] = {};
     if (n < N) {
-        for (int c0 = wv; c0 < C; c0 += 32) {
-            float v[8];
+        for (int c0 = g; c0 < C; c0 += 8 * NG) {
+            float v[8][CPL];
 #pragma unroll
             for (int u = 0; u < 8; ++u) {
-                const int c = c0 + 4 * u;
-                v[u] = c < C ? P[(size_t)c * N + n] : 0.f;
+                const int c = c0 + NG * u;
+                if constexpr (VEC) {
+                    const f32x4 t = c < C ? *reinterpret_cast<const f32x4*>(P + (size_t)c * N + n) : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) v[u][e] = t[e];
+                } else {
+                    v[u][0] = c < C ? P[(size_t)c * N + n] : 0.f;
+                }
             }
 #pragma unroll
-            for (int u = 0; u < 8; ++u) s += v[u];
+            for (int u = 0; u < 8; ++u)
+#pragma unroll
+                for (int e = 0; e < CPL; ++e) s[e] += v[u][e];
         }
     }
-    red[wv][lane] = s;
+#pragma unroll
+    for (int e = 0; e < CPL; ++e) red[g][cl + e] = s[e];
     __syncthreads();
-    if (wv == 0 && n < N) {
-        float r = alpha * ((red[0][lane] + red[1][lane]) + (red[2][lane] + red[3][lane]));
-        if (beta != 0.f) r = fmaf(beta, y[n], r);  // y untouched when beta == 0
-        y[n] = r;
+    if (tid < 64 && blockIdx.x * 64 + tid < N) {
+        float t = 0.f;
+#pragma unroll
+        for (int h = 0; h < NG; ++h) t += red[h][tid];
+        const int col = blockIdx.x * 64 + tid;
+        float r = alpha * t;
+        if (beta != 0.f) r = fmaf(beta, y[col], r);  // y untouched when beta == 0
+        y[col] = r;
     }
 }
 
@@ -521,7 +541,10 @@ hipError_t launch_gemv_f32_t(const float* A, const float* x, float* y, int M, in
     else
         hipLaunchKernelGGL(k_gemv_t_partial<false>, dim3((unsigned)((N + 63) / 64), (unsigned)C), dim3(256), 0, s,
                            A, x, ws, M, N, lda, R);
-    hipLaunchKernelGGL(k_gemv_t_reduce, dim3((unsigned)((N + 63) / 64)), dim3(256), 0, s, ws, y, N, C, alpha, beta);
+    if (N % 4 == 0)  // the partials then start 16-byte aligned (ws is)
+        hipLaunchKernelGGL(k_gemv_t_reduce<true>, dim3((unsigned)((N + 63) / 64)), dim3(256), 0, s, ws, y, N, C, alpha, beta);
+    else
+        hipLaunchKernelGGL(k_gemv_t_reduce<false>, dim3((unsigned)((N + 63) / 64)), dim3(256), 0, s, ws, y, N, C, alpha, beta);
     return hipGetLastError();
 }
 

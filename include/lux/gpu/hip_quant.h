@@ -277,11 +277,12 @@ LuxBackendError lux_hip_rms_norm(LuxBackendContext* ctx, const LuxHipRmsNormPara
  * QUANTIZE_X).  The result is bit-identical to lux_hip_rms_norm into a buffer of
  * desc->x_dtype followed by lux_hip_qmatmul_ex.  At m == 1 with int4 weights, SCALE_F16,
  * x_dtype F16, flags 0 and k <= 8192 on the GEMV's fast path (k % 32 == 0, group_size a
- * power-of-two multiple of 32 with an even number of groups per row), the GEMV computes
- * the normalisation in its prologue (one launch; a decode step's rms_norm kernel and
- * its output round trip disappear).  Other descriptors run rms_norm and then the
- * matmul, with xn in the context workspace.  Errors as lux_hip_rms_norm and
- * lux_hip_qmatmul_ex. */
+ * power-of-two multiple of 32 with an even number of groups per row), where the GEMV
+ * streams whole rows per wave (more than 16 rows per CU, or k < 4096: the gate/up and
+ * QKV projections of a decode step), the GEMV computes the normalisation in its
+ * prologue (one launch; the rms_norm kernel and its output round trip disappear).
+ * Other descriptors run rms_norm and then the matmul, with xn in the context
+ * workspace.  Errors as lux_hip_rms_norm and lux_hip_qmatmul_ex. */
 LuxBackendError lux_hip_rms_norm_qmatmul(LuxBackendContext* ctx, const LuxHipRmsNormParams* norm,
                                          LuxBackendBuffer* gamma, const LuxHipQMatmulDesc* desc,
                                          LuxBackendBuffer* w, LuxBackendBuffer* w_scales,

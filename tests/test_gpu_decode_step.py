@@ -131,7 +131,7 @@ def _norm_input(r, m, k, xdt):
     return x
 
 
-def _fused_vs_two_calls(ctx, r, desc, xin, xdt, wp, s, epi, ydt, coding_bias=False):
+def _fused_vs_two_calls(ctx, r, desc, xin, xdt, wp, s, epi, ydt):
     """Run lux_hip_rms_norm_qmatmul and lux_hip_rms_norm + lux_hip_qmatmul_ex on the same
     inputs; return both outputs as raw bits (they must be identical) and the normalised row."""
     m, k, n_out = desc.m, desc.k, desc.n_out
@@ -163,10 +163,11 @@ def _fused_vs_two_calls(ctx, r, desc, xin, xdt, wp, s, epi, ydt, coding_bias=Fal
     (4128, "f16", W.EPI_NONE, W.F16, 0),          # k not a multiple of 256: ragged last pass
     (96, "f32", W.EPI_NONE, W.F32, 0)])           # fewer elements than threads
 def test_rms_norm_qmatmul_fused_gemv_bit_identical(ctx, k, xdt, epi, ydt, coding):
-    """m = 1, int4, fp16 scales, fp16 activations: the GEMV normalises the row in its prologue.
-    The output must equal rms_norm followed by qmatmul_ex bit for bit, and the oracle."""
+    """m = 1, int4, fp16 scales, fp16 activations: the GEMV normalises the row in its prologue
+    (4160 rows: more than 16 per CU, so whole rows per wave). The output must equal rms_norm
+    followed by qmatmul_ex bit for bit, and the oracle."""
     r = rng(k * 7 + len(xdt) + epi)
-    n_out, gs = 1030, 32
+    n_out, gs = 4160, 32
     _, Wp, s = int4_weights(r, n_out, k, gs, coding)
     xin = _norm_input(r, 1, k, xdt)
     desc = W.qdesc(n_out, k, 1, 4, gs, coding, W.SCALE_F16, W.F16, ydt)
@@ -182,7 +183,7 @@ def test_rms_norm_qmatmul_fused_gemv_bit_identical(ctx, k, xdt, epi, ydt, coding
         compare(got.astype(np.float64), round_to(ref.astype(np.float32), yname), f"rms_norm_qmatmul k{k}")
 
 
-@pytest.mark.parametrize("case", ["small_m", "k16384", "scale_f32", "x_f32", "w8", "w4a8_qx"])
+@pytest.mark.parametrize("case", ["small_m", "k16384", "k_halves", "scale_f32", "x_f32", "w8", "w4a8_qx"])
 def test_rms_norm_qmatmul_two_launch_routes(ctx, case):
     """Descriptors outside the fused GEMV run rms_norm into the workspace, then the matmul:
     still bit-identical to the two separate calls."""
@@ -192,6 +193,8 @@ def test_rms_norm_qmatmul_two_launch_routes(ctx, case):
         m, epi = 5, W.EPI_SILU_MUL
     elif case == "k16384":
         k = 16384
+    elif case == "k_halves":  # few long rows: the plain GEMV splits k, so both kernels run
+        k = 8192
     elif case == "scale_f32":
         sf = W.SCALE_F32
     elif case == "x_f32":

@@ -3,8 +3,9 @@
 A caller that sets lux_hip_context_set_synchronous(ctx, 0) and its own stream may capture
 the plugin's launches in a graph (bench.py times every config that way).  One graph holds
 a decode step (rms_norm -> int4 gate/up GEMM with SILU_MUL -> int4 down GEMV -> residual
-op_add_f32), a large-m int4 GEMM with bf16 activations (pre-pass + MFMA GEMM, workspace)
-and a W4A8 GEMM with QUANTIZE_X (per-token quantizer + int8 MFMA, workspace).  It is
+op_add_f32), a large-m int4 GEMM with bf16 activations (pre-pass + MFMA GEMM, workspace),
+a W4A8 GEMM with QUANTIZE_X (per-token quantizer + int8 MFMA, workspace) and the gate/up
+GEMV with rms_norm in its prologue (lux_hip_rms_norm_qmatmul).  It is
 replayed three times with new inputs written by eager torch work between the replays;
 every replay must equal, bit for bit, the same ops run eagerly in synchronous mode (the
 kernels are deterministic, so graph and eager results are identical).
@@ -44,7 +45,8 @@ def test_graph_replays_match_eager(plugin):
         d_l = W.qdesc(nl, kl, ml, 4, 32, 0, W.SCALE_F16, W.BF16, W.BF16)
         d_q = W.qdesc(nq, kq, mq, 4, 128, 1, W.SCALE_F16, W.F32, W.F16, W.QFLAG_QUANTIZE_X)
         shapes = {"d": (hidden * 4, np.float32, (hidden,)), "res": (hidden * 4, np.float32, (hidden,)),
-                  "large": (ml * nl * 2, np.uint16, (ml, nl)), "w4a8": (mq * nq * 2, np.uint16, (mq, nq))}
+                  "large": (ml * nl * 2, np.uint16, (ml, nl)), "w4a8": (mq * nq * 2, np.uint16, (mq, nq)),
+                  "fused": (inter * 2, np.float16, (inter,))}
 
         def outputs():
             return {k: c.alloc(v[0]) for k, v in shapes.items()}
@@ -56,6 +58,7 @@ def test_graph_replays_match_eager(plugin):
             c.binary_f32("add", xb, o["d"], o["res"], hidden)
             c.qmatmul(d_l, wl, s_l, xlb, None, o["large"])
             c.qmatmul(d_q, wq, s_q, xqb, None, o["w4a8"])
+            c.rms_norm_qmatmul(xb, gb, 1e-6, W.F32, d_gu, wgu, s_gu, W.EPI_SILU_MUL, None, None, o["fused"])
 
         def fetch(o):
             return {k: c.download(o[k], v[1], v[2]) for k, v in shapes.items()}
@@ -86,6 +89,8 @@ def test_graph_replays_match_eager(plugin):
             ref = fetch(oe)
             for k in shapes:
                 assert np.array_equal(got[k].view(np.uint8), ref[k].view(np.uint8)), f"replay {i}: {k}"
+            # rms_norm inside the gate/up GEMV gives the bits of the separate rms_norm
+            assert np.array_equal(got["fused"].view(np.uint16), c.download(hb, np.float16, (inter,)).view(np.uint16))
             if prev is not None:  # the replay saw the new inputs
                 assert not np.array_equal(got["res"], prev["res"])
                 assert not np.array_equal(got["large"], prev["large"])

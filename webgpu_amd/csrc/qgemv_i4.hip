@@ -61,25 +61,31 @@ __device__ __forceinline__ float dot_slice_sub(const uint32_t (&q)[4], const f16
 // / K + eps), with k_rms_norm's arithmetic in k_rms_norm's order (thread t sums elements
 // t + 256 j, j ascending, then the DPP wave sum and the four wave sums in a fixed order),
 // so the staged row is bit-identical to what k_rms_norm would have written.
-template <int SPL, int RW, int D, ScaleKind SK, YKind YK, bool XOR, bool SM, bool RN>
+// KS = 2 (few, long rows: the decode down-projection): waves w and w + 2 of a block take
+// the same RW rows, w the first half of k and w + 2 the second, so each wave has twice
+// the rows to pipeline; the two halves' sums meet in LDS and are added in that order.
+template <int SPL, int RW, int D, ScaleKind SK, YKind YK, bool XOR, bool SM, bool RN, int KS = 1>
 __global__ __launch_bounds__(256) void k_qgemv_i4_f16(const u32x4* __restrict__ W,
                                                       const void* __restrict__ S,
                                                       const f16* __restrict__ x,
                                                       void* __restrict__ y, int n_out, int K,
                                                       int spg_shift, uint32_t xor_mask, EpiArgs epi, RnArgs rn) {
-    __shared__ u32x4 xs[SPL * 256];  // K <= SPL * 2048 halves
-    const int lane = threadIdx.x & 63;
-    const int row0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * RW;
+    static_assert(KS == 1 || (KS == 2 && !SM && !RN), "k halves: plain rows only");
+    __shared__ u32x4 xs[KS * SPL * 256];  // K <= KS * SPL * 2048 halves
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int row0 = (KS == 1 ? blockIdx.x * 4 + wave : blockIdx.x * 2 + (wave & 1)) * RW;
     const bool active = row0 < n_out;
     const int nrows = min(RW, n_out - row0);
     const int s_row = K >> 5;        // slices per row
     const int g_row = s_row >> spg_shift;  // groups per row (slices per group: a power of two)
+    const int s_part = s_row / KS;   // slices of the wave's part of k (KS = 2: s_row is even)
+    const int s_base = KS == 1 ? 0 : (wave >> 1) * s_part;
 
     // Load order matters: vmcnt retires loads in issue order, so the block's x chunks
     // (L2 hits) go first, then the first D rows of weight slices and raw scales.  All
     // addresses are clamped to valid ones; out-of-range slices get x = 0 after the
     // loads, and rows past the wave's share are never computed or stored.
-    u32x4 xv[SPL];
+    u32x4 xv[KS * SPL];
     constexpr int NJ = RN ? 8 * SPL : 1;  // RN: row elements per thread (K <= 2048 * SPL)
     float xe[NJ], ge[NJ];
     if constexpr (RN) {
@@ -98,7 +104,7 @@ __global__ __launch_bounds__(256) void k_qgemv_i4_f16(const u32x4* __restrict__ 
         for (int j = 0; j < NJ; ++j) ge[j] = rn.gamma[min((int)threadIdx.x + 256 * j, last)];
     } else {
 #pragma unroll
-        for (int j = 0; j < SPL; ++j) {
+        for (int j = 0; j < KS * SPL; ++j) {
             const int c = threadIdx.x + 256 * j;
             xv[j] = c < K / 8 ? reinterpret_cast<const u32x4*>(x)[c] : u32x4{0u, 0u, 0u, 0u};
         }
@@ -106,7 +112,7 @@ __global__ __launch_bounds__(256) void k_qgemv_i4_f16(const u32x4* __restrict__ 
     __builtin_amdgcn_sched_barrier(0);  // keep x loads ahead of the weight stream
     int sl[SPL];
 #pragma unroll
-    for (int j = 0; j < SPL; ++j) sl[j] = min(lane + 64 * j, s_row - 1);
+    for (int j = 0; j < SPL; ++j) sl[j] = s_base + min(lane + 64 * j, s_part - 1);
 
     u32x4 q[RW][SPL];
     uint32_t sraw[RW][SPL];
@@ -149,13 +155,14 @@ __global__ __launch_bounds__(256) void k_qgemv_i4_f16(const u32x4* __restrict__ 
         }
     } else {
 #pragma unroll
-        for (int j = 0; j < SPL; ++j) {
+        for (int j = 0; j < KS * SPL; ++j) {
             const int c = threadIdx.x + 256 * j;
             if (c < K / 8) xs[c] = xv[j];
         }
     }
     __syncthreads();  // every wave of the block reaches this before any returns
-    if (!active) return;
+    // KS = 2: waves without rows still run (on clamped rows) to the halves' barrier
+    if (KS == 1 && !active) return;
 
     // x pairs in decode order and, per slice, -8 * sum(x) (offset-binary q = n - 8).
     f16x2 xp[SPL][4][4];
@@ -163,7 +170,7 @@ __global__ __launch_bounds__(256) void k_qgemv_i4_f16(const u32x4* __restrict__ 
     const f16x2 ONES = {(f16)1.0f, (f16)1.0f};
 #pragma unroll
     for (int j = 0; j < SPL; ++j) {
-        const uint32_t keep = lane + 64 * j < s_row ? ~0u : 0u;  // bitwise: no branch
+        const uint32_t keep = lane + 64 * j < s_part ? ~0u : 0u;  // bitwise: no branch
         float sx = 0.f;
 #pragma unroll
         for (int w = 0; w < 4; ++w) {
@@ -205,6 +212,12 @@ __global__ __launch_bounds__(256) void k_qgemv_i4_f16(const u32x4* __restrict__ 
     if constexpr (SM) {
         const float up = __shfl_down(res, 1, 64);  // the pair's up row sits in the next lane
         if (lane < nrows && !(lane & 1)) store_y<YK>(y, (row0 + lane) >> 1, silu_f(res) * up);
+    } else if constexpr (KS == 2) {
+        __shared__ float hi_half[2][64];
+        if (wave >= 2) hi_half[wave & 1][lane] = res;
+        __syncthreads();
+        const float tot = res + hi_half[wave & 1][lane];
+        if (wave < 2 && lane < nrows) store_y<YK>(y, row0 + lane, apply_epi(tot, epi, 0, row0 + lane, n_out));
     } else {
         if (lane < nrows) store_y<YK>(y, row0 + lane, apply_epi(res, epi, 0, row0 + lane, n_out));
     }
@@ -235,9 +248,9 @@ __global__ __launch_bounds__(256) void k_qgemv_i4_generic(const uint32_t* __rest
     if (lane == 0) store_y<YK>(y, row, apply_epi(acc, epi, 0, row, n_out));
 }
 
-template <int SPL, int RW, int D, ScaleKind SK, YKind YK, bool RN>
+template <int SPL, int RW, int D, ScaleKind SK, YKind YK, bool RN, int KS = 1>
 static void launch_rwd(const QArgs& a, hipStream_t s) {
-    const int waves = (a.n_out + RW - 1) / RW;
+    const int waves = (a.n_out + RW - 1) / RW * KS;
     const dim3 grid((waves + 3) / 4), block(256);
     const u32x4* w = reinterpret_cast<const u32x4*>(a.w);
     const f16* x = reinterpret_cast<const f16*>(a.x);
@@ -245,6 +258,11 @@ static void launch_rwd(const QArgs& a, hipStream_t s) {
     auto go = [&](auto kern) {
         hipLaunchKernelGGL(kern, grid, block, 0, s, w, a.s, x, a.y, a.n_out, a.k, shift, a.xor_mask, a.epi, a.rn);
     };
+    if constexpr (KS == 2) {
+        if (a.xor_mask) go(k_qgemv_i4_f16<SPL, RW, D, SK, YK, true, false, false, 2>);
+        else go(k_qgemv_i4_f16<SPL, RW, D, SK, YK, false, false, false, 2>);
+        return;
+    }
     const bool sm = a.epi.kind == (int)Epi::SiluMul;
     if constexpr (RW % 2 == 0) {
         if (sm) {
@@ -260,31 +278,45 @@ static void launch_rwd(const QArgs& a, hipStream_t s) {
 // Two rows of prefetch (issue row r+2, then compute row r) measured best on MI355X for
 // config 2 (6.9 us against 7.0 us with one row); issuing all rows up front bunches the
 // arrivals and lengthens the tail (8.6 us).
-template <int SPL, int RW, ScaleKind SK, YKind YK, bool RN>
+template <int SPL, int RW, ScaleKind SK, YKind YK, bool RN, int KS = 1>
 static void launch_rw(const QArgs& a, hipStream_t s) {
-    launch_rwd<SPL, RW, 2, SK, YK, RN>(a, s);
+    launch_rwd<SPL, RW, 2, SK, YK, RN, KS>(a, s);
 }
 
 // Rows per wave: enough for 8 waves per CU with equal shares (14336 rows on 256
 // CUs -> 7 rows per wave, 2048 waves); capped so the weight registers
 // (RW * SPL * 4 VGPRs) stay within 64.
-template <int SPL, ScaleKind SK, YKind YK, bool RN>
+template <int SPL, ScaleKind SK, YKind YK, bool RN, int KS = 1>
 static void launch_fast(const QArgs& a, hipStream_t s) {
     constexpr int RWMAX = SPL <= 2 ? 8 : 16 / SPL;
     const int target_waves = device_cus() * 8;
-    int rw = (a.n_out + target_waves - 1) / target_waves;
+    int rw = (KS * a.n_out + target_waves - 1) / target_waves;
     rw = rw < 1 ? 1 : (rw > RWMAX ? RWMAX : rw);
     if (a.epi.kind == (int)Epi::SiluMul) rw += rw & 1;  // whole gate/up pairs per wave (RWMAX is even)
     switch (rw) {
-        case 1: launch_rw<SPL, 1, SK, YK, RN>(a, s); break;
-        case 2: launch_rw<SPL, 2, SK, YK, RN>(a, s); break;
-        case 3: if constexpr (RWMAX >= 3) launch_rw<SPL, 3, SK, YK, RN>(a, s); break;
-        case 4: if constexpr (RWMAX >= 4) launch_rw<SPL, 4, SK, YK, RN>(a, s); break;
-        case 5: if constexpr (RWMAX >= 5) launch_rw<SPL, 5, SK, YK, RN>(a, s); break;
-        case 6: if constexpr (RWMAX >= 6) launch_rw<SPL, 6, SK, YK, RN>(a, s); break;
-        case 7: if constexpr (RWMAX >= 7) launch_rw<SPL, 7, SK, YK, RN>(a, s); break;
-        default: if constexpr (RWMAX >= 8) launch_rw<SPL, 8, SK, YK, RN>(a, s); break;
+        case 1: launch_rw<SPL, 1, SK, YK, RN, KS>(a, s); break;
+        case 2: launch_rw<SPL, 2, SK, YK, RN, KS>(a, s); break;
+        case 3: if constexpr (RWMAX >= 3) launch_rw<SPL, 3, SK, YK, RN, KS>(a, s); break;
+        case 4: if constexpr (RWMAX >= 4) launch_rw<SPL, 4, SK, YK, RN, KS>(a, s); break;
+        case 5: if constexpr (RWMAX >= 5) launch_rw<SPL, 5, SK, YK, RN, KS>(a, s); break;
+        case 6: if constexpr (RWMAX >= 6) launch_rw<SPL, 6, SK, YK, RN, KS>(a, s); break;
+        case 7: if constexpr (RWMAX >= 7) launch_rw<SPL, 7, SK, YK, RN, KS>(a, s); break;
+        default: if constexpr (RWMAX >= 8) launch_rw<SPL, 8, SK, YK, RN, KS>(a, s); break;
     }
+}
+
+// Halves of k per row (KS = 2) when rows are few and long: at 8 waves per CU each wave
+// would get at most two rows (nothing to overlap its math with), k is at least 4096 and
+// splits into whole slices, and each half fits four slices per lane.  fp16 scales, no
+// gated pairs, no fused rms_norm.
+static bool use_k_halves(const QArgs& a) {
+    static const bool off = [] {  // LUX_HIP_GEMV_NO_KSPLIT=1: whole rows per wave (A/B timing)
+        const char* e = getenv("LUX_HIP_GEMV_NO_KSPLIT");
+        return e && e[0] == '1';
+    }();
+    const int target_waves = device_cus() * 8;
+    return !off && a.scale_kind == ScaleKind::F16 && a.epi.kind != (int)Epi::SiluMul && !a.rn.gamma &&
+           a.n_out <= 2 * target_waves && a.k >= 4096 && a.k % 64 == 0 && a.k / 2 <= 8192;
 }
 
 // RN (the GEMV normalises its own row): one to four slices per lane (k <= 8192), so that
@@ -292,6 +324,15 @@ static void launch_fast(const QArgs& a, hipStream_t s) {
 template <ScaleKind SK, YKind YK, bool RN>
 static bool dispatch_spl(const QArgs& a, hipStream_t s) {
     const int slices = a.k / 32;
+    if constexpr (SK == ScaleKind::F16 && !RN) {
+        if (use_k_halves(a)) {
+            const int sph = (slices / 2 + 63) / 64;  // slices per lane in each half
+            if (sph <= 1) launch_fast<1, SK, YK, RN, 2>(a, s);
+            else if (sph <= 2) launch_fast<2, SK, YK, RN, 2>(a, s);
+            else launch_fast<4, SK, YK, RN, 2>(a, s);
+            return true;
+        }
+    }
     const int spl = (slices + 63) / 64;
     if (spl <= 1) launch_fast<1, SK, YK, RN>(a, s);
     else if (spl <= 2) launch_fast<2, SK, YK, RN>(a, s);
@@ -347,10 +388,15 @@ bool qgemv_i4_fast(const QArgs& a) {
            ((uintptr_t)a.s & 3u) == 0;  // fp16 scales are read as aligned u32 pairs
 }
 
+// The fused form stays bit-identical to rms_norm followed by the plain GEMV only where the
+// plain GEMV gives whole rows to one wave; shapes it splits into k halves run both kernels.
 bool qgemv_i4_rn_supported(const QArgs& a) {
+    QArgs plain = a;
+    plain.rn.gamma = nullptr;
     QArgs b = a;
     if (!b.rn.gamma) b.rn.gamma = reinterpret_cast<const float*>(16);  // only the x-alignment test differs
-    return a.m == 1 && a.wbits == 4 && a.scale_kind == ScaleKind::F16 && a.k <= 8192 && qgemv_i4_fast(b);
+    return a.m == 1 && a.wbits == 4 && a.scale_kind == ScaleKind::F16 && a.k <= 8192 && qgemv_i4_fast(b) &&
+           !use_k_halves(plain);
 }
 
 hipError_t launch_qgemv_i4(const QArgs& a, hipStream_t s) {

@@ -101,6 +101,31 @@ def test_w4a8_scaled_shapes(ctx, n_out, K, m, gs, sfmt, y):
     compare(got, round_to(ref.astype(np.float32), y), f"W4A8 scaled {n_out}x{K} m{m} g{gs} {y}")
 
 
+@pytest.mark.parametrize("n_out,K,m,coding,y", [(11008, 4096, 256, 1, "f16"), (11008, 4096, 256, 0, "f32"),
+                                                (11000, 4096, 250, 0, "bf16"), (130, 384, 65, 0, "bf16"),
+                                                (64, 128, 3, 1, "f32")])
+def test_w4a8_fp16_scales_same_bits_as_fp32_scales(ctx, n_out, K, m, coding, y):
+    """g128 with fp16 scales decodes nibbles to 16 q and stages s / 16 (config-5-sized shapes:
+    in 11-wave blocks, the group scaling a stage late); fp32 scales of the same values take
+    the plain decode in 4-wave blocks. Both feed every fma the same product in the same group
+    order, so the outputs must agree bit for bit; and the fp16-scale result matches the exact
+    group sums. 11000 x 250: a partial last row block and a partial last token block."""
+    r = rng(n_out * 5 + K + m + coding)
+    q, Wp, s16, a8, ascale = _inputs(r, n_out, K, m, 128, coding)
+    ycode, ynp = {"f16": (W.F16, np.float16), "f32": (W.F32, np.float32), "bf16": (W.BF16, np.uint16)}[y]
+    wb, xb, asb = ctx.upload(Wp), ctx.upload(a8), ctx.upload(ascale)
+    outs = []
+    for sfmt, sbuf in ((W.SCALE_F16, s16), (W.SCALE_F32, s16.astype(np.float32))):
+        yb = ctx.alloc(m * n_out * np.dtype(ynp).itemsize)
+        ctx.qmatmul(W.qdesc(n_out, K, m, 4, 128, coding, sfmt, W.I8, ycode), wb, ctx.upload(sbuf), xb, asb, yb)
+        outs.append(ctx.download(yb, ynp, (m, n_out)))
+    assert np.array_equal(outs[0].view(np.uint8), outs[1].view(np.uint8))
+    got = (bf16_to_f32(outs[0]) if y == "bf16" else outs[0].astype(np.float32)).astype(np.float64)
+    P = oracle.w4a8_group_partials(Wp, a8, 128, coding).astype(np.float64)      # [m, n, G]
+    ref = (P * s16.astype(np.float64)[None, :, :]).sum(axis=2) * ascale.astype(np.float64)[:, None]
+    compare(got, round_to(ref.astype(np.float32), y), f"W4A8 fp16 scales {n_out}x{K} m{m} coding {coding}")
+
+
 def test_w4a8_rejects(ctx):
     r = rng(1)
     q, Wp, s, a8, ascale = _inputs(r, 32, 128, 4, 128, 1)

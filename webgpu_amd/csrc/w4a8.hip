@@ -15,22 +15,28 @@
 //                              group order g = 0 .. G-1.
 //
 // Tiling (gfx950, v_mfma_i32_16x16x64_i8, A = weight rows, B = tokens, K = 64):
-//   block = 4 waves = 64 weight rows x 64 tokens; wave = 16 rows (one row tile) x 64
-//   tokens (4 token tiles, 4 independent MFMA chains).  Small blocks let up to three
-//   of them share a CU (config 5: 688 blocks on 256 CUs), so one block's barrier and
-//   memory waits overlap another's MFMAs.  Per 128-k stage a lane (row l % 16,
-//   quarter q = l / 16) loads 16 packed bytes per row tile = k 32 q .. 32 q + 31 and
-//   sign-extends the nibbles into bytes with a SWAR add/xor, in the order
-//   (k0 k2 k4 k6 | k1 k3 k5 k7) per 8 k; the two MFMA k-steps take nibbles 0-15 and
-//   16-31.  Activations of the stage (64 tokens x 128 B) are loaded as coalesced
-//   16-B chunks PD stages ahead,
-//   byte-permuted into the same order and written to LDS; all four waves read them.
-//   The weights are the only operand each wave owns, so nothing is decoded twice.
+//   a wave = 16 rows (one row tile) x 64 tokens (4 token tiles, 4 independent MFMA
+//   chains); a block = NWB waves over 16 NWB rows and the same 64 tokens.  NWB = 4 lets
+//   up to three blocks share a CU, so one block's barrier and memory waits overlap
+//   another's MFMAs; NWB = 11 (176 rows, one block per CU; config 5: 252 blocks on 256
+//   CUs) stages each token block's activations for 176 rows instead of 64.  Per 128-k
+//   stage a lane (row l % 16, quarter q = l / 16) loads 16 packed bytes per row tile =
+//   k 32 q .. 32 q + 31 and turns the nibbles into bytes in the order
+//   (k0 k2 k4 k6 | k1 k3 k5 k7) per 8 k: sign-extended by a SWAR add/xor, or, for the
+//   scaled g128 path with fp16 scales, left as 16 q in the top of each byte.  The two
+//   MFMA k-steps take nibbles 0-15 and 16-31.  Activations of the stage (64 tokens x
+//   128 B) are loaded as coalesced 16-B chunks PD stages ahead, byte-permuted into the
+//   same order and written to LDS; all the block's waves read them.  The weights are
+//   the only operand each wave owns, so nothing is decoded twice.
+//   The scaled output costs two VALU per int32 sum and group (convert, fma), as many
+//   issue cycles as the group's MFMAs; with NWB = 11 it runs a stage late, after the
+//   next stage's MFMAs, so it never waits on a result just issued.
 //
 // Block order is XCD-aware: consecutive workgroups go to the 8 XCDs in turn, so the
 // token blocks of one row block are given block ids that land on the same XCD and
 // share its L2 copy of the block's weight rows.
 #include <algorithm>
+#include <type_traits>
 
 #include "common.hpp"
 
@@ -41,12 +47,22 @@ namespace {
 constexpr int GK = 128;    // k per stage (one group of 128 when gs == 128)
 constexpr int AROW = GK + 16;  // LDS bytes per staged token row (padded)
 constexpr int RT = 1;      // 16-row MFMA tiles per wave
-constexpr int BR = 64 * RT;  // weight rows per block (4 waves)
 constexpr int BT = 64;     // tokens per block
 constexpr int NXCD = 8;
 constexpr int PD = 3;      // stages fetched ahead
 constexpr int GMAX = 128;  // groups per row held in LDS (scaled output)
 constexpr int SCH = 8;     // 16-byte scale chunks per thread (block region <= 32 KB)
+
+// 8 nibbles (k0..k7) of one word -> 16 x signed values as bytes, in the same order: the
+// nibbles moved to the top of each byte (16 q for two's complement, 16 q + 128 for
+// offset-binary, which the xor with 0x80 per byte turns into 16 q).  3 VALU per word
+// instead of 7; the group partials come out 16 x larger (exact: |16 P_g| <= 2^21 at
+// 128 k), and the staged scale is s / 16 (exact for fp16 scales), so every fma
+// s * P_g + acc sees the same operands' product and rounds the same.
+__device__ __forceinline__ void unpack_i4_to_i8x16(uint32_t w, uint32_t xm, uint32_t& lo, uint32_t& hi) {
+    lo = ((w << 4) & 0xF0F0F0F0u) ^ xm;
+    hi = (w & 0xF0F0F0F0u) ^ xm;
+}
 
 // 8 nibbles (k0..k7) of one word -> signed bytes (k0, k2, k4, k6) and (k1, k3, k5, k7).
 // Offset-binary u = q + 8: byte = (u + 0x78) ^ 0x80.  Two's complement t: u = t ^ 8,
@@ -75,13 +91,17 @@ __device__ __forceinline__ u32x4 perm16(u32x4 v) {
 
 // MODE 0: full-K int32; 1: per-group int32 partials; 2: scaled fp output.
 // ONEG: group size == 128, every stage is one whole group (no carry across stages).
-template <int WB, int MODE, bool ONEG, ScaleKind SK, YKind YK>
-__global__ __launch_bounds__(256, MODE == 1 ? 2 : 3) void k_w4a8(const uint8_t* __restrict__ W,
+template <int WB, int MODE, bool ONEG, ScaleKind SK, YKind YK, int NWB = 4, bool DEF = false>
+__global__ __launch_bounds__(64 * NWB, NWB == 4 ? (MODE == 1 ? 2 : 3) : 1) void k_w4a8(const uint8_t* __restrict__ W,
                                               const void* __restrict__ S,
                                               const int8_t* __restrict__ A,
                                               const float* __restrict__ AS,
                                               void* __restrict__ Y, int M, int N, int K, int gs,
                                               uint32_t tc, int nrb, int ntb, int vec_y) {
+    constexpr int NTB = 64 * NWB;                      // threads
+    constexpr int BR = 16 * RT * NWB;                  // weight rows of the block
+    constexpr int CPT = (BT * 8 + NTB - 1) / NTB;      // activation chunks per thread and stage
+    constexpr int SCHB = (256 * SCH + NTB - 1) / NTB;  // scale chunks per thread (<= 32 KB)
     __shared__ __attribute__((aligned(16))) uint8_t as[2][BT][AROW];
     extern __shared__ __attribute__((aligned(16))) float ssT[];  // MODE 2: [G][BR] scales
 
@@ -94,6 +114,13 @@ __global__ __launch_bounds__(256, MODE == 1 ? 2 : 3) void k_w4a8(const uint8_t* 
     const int r16 = lane & 15, q = lane >> 4;
     const int G = K / gs;
     const int nst = K / GK;
+    // Scaled output, one group per stage, fp16 scales: decode to 16 q (unpack_i4_to_i8x16).
+    constexpr bool X16 = WB == 4 && MODE == 2 && ONEG && SK == ScaleKind::F16;
+    // DEFER: the group scaling of stage s runs in stage s + 1, after that stage's MFMAs, so
+    // the conversions read results finished a stage earlier; PD partial sets rotate with
+    // the unrolled stages (same fma order, same results).
+    constexpr bool DEFER = X16 && DEF;
+    const uint32_t xm = tc ? 0u : 0x80808080u;
 
     // Raw buffer loads: each lane keeps a fixed byte offset (voffset) and the stage
     // moves a uniform offset (soffset, scalar arithmetic only).  Reads past the end of
@@ -107,10 +134,14 @@ __global__ __launch_bounds__(256, MODE == 1 ? 2 : 3) void k_w4a8(const uint8_t* 
     const __amdgpu_buffer_rsrc_t ra =
         __builtin_amdgcn_make_buffer_rsrc(const_cast<int8_t*>(A), (short)0, (int)((size_t)M * K), 0x00020000);
     const int wv0 = (n0 + r16) * rowb + 16 * LW * q;
-    // activation chunks of a stage: 64 tokens x 8 chunks of 16 B; thread: token tid / 8
-    // and tid / 8 + 32, chunk tid % 8 (8 lanes read one token's 128 contiguous bytes)
-    const int tk = tid >> 3, part = tid & 7;
-    const int av0 = (tb + tk) * K + 16 * part, av1 = av0 + 32 * K;
+    // activation chunks of a stage: 64 tokens x 8 chunks of 16 B; chunk c = tid + NTB i is
+    // token c / 8, part c % 8 (8 lanes read one token's 128 contiguous bytes)
+    int av[CPT];
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) {
+        const int c = tid + NTB * i;
+        av[i] = (tb + (c >> 3)) * K + 16 * (c & 7);
+    }
 
     auto ldw = [&](u32x4 (&w)[RT * LW], int st) {
         const int so = __builtin_amdgcn_readfirstlane(st * (GK / 8 * WB));
@@ -121,16 +152,22 @@ __global__ __launch_bounds__(256, MODE == 1 ? 2 : 3) void k_w4a8(const uint8_t* 
                 w[f * LW + h] = __builtin_bit_cast(
                     u32x4, __builtin_amdgcn_raw_buffer_load_b128(rw, wv0 + f * 16 * rowb + 16 * h, so, 0));
     };
-    auto lda = [&](u32x4 (&a)[2], int st) {
+    auto lda = [&](u32x4 (&a)[CPT], int st) {
         const int so = __builtin_amdgcn_readfirstlane(st * GK);
-        a[0] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(ra, av0, so, 0));
-        a[1] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(ra, av1, so, 0));
+#pragma unroll
+        for (int i = 0; i < CPT; ++i)
+            if (NTB * (i + 1) <= BT * 8 || tid + NTB * i < BT * 8)  // whole waves
+                a[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(ra, av[i], so, 0));
     };
     // int4 weights decode to (k0 k2 k4 k6 | k1 k3 k5 k7) per 8 k, so the activations are
     // permuted the same way; int8 weights keep the natural order on both sides.
-    auto sta = [&](int buf, const u32x4 (&a)[2]) {
-        *reinterpret_cast<u32x4*>(&as[buf][tk][16 * part]) = WB == 4 ? perm16(a[0]) : a[0];
-        *reinterpret_cast<u32x4*>(&as[buf][tk + 32][16 * part]) = WB == 4 ? perm16(a[1]) : a[1];
+    auto sta = [&](int buf, const u32x4 (&a)[CPT]) {
+#pragma unroll
+        for (int i = 0; i < CPT; ++i) {
+            const int c = tid + NTB * i;
+            if (NTB * (i + 1) <= BT * 8 || c < BT * 8)
+                *reinterpret_cast<u32x4*>(&as[buf][c >> 3][16 * (c & 7)]) = WB == 4 ? perm16(a[i]) : a[i];
+        }
     };
 
     i32x4 iacc[RT][4];
@@ -146,7 +183,7 @@ __global__ __launch_bounds__(256, MODE == 1 ? 2 : 3) void k_w4a8(const uint8_t* 
     // The block's group scales (rows rb * BR .. + BR - 1 of [N][G]: one contiguous
     // region) are loaded first, then the first PD stages; then the scales are
     // converted to fp32 and transposed into ssT[g][row] (rows past N read zeros).
-    u32x4 sv[SCH];
+    u32x4 sv[SCHB];
     constexpr int SB = SK == ScaleKind::F16 ? 2 : SK == ScaleKind::GroupScale ? 16 : 4;
     constexpr int EPC = SK == ScaleKind::F16 ? 8 : SK == ScaleKind::GroupScale ? 1 : 4;  // per 16 B
     const int nch = BR * G * SB / 16;
@@ -155,8 +192,8 @@ __global__ __launch_bounds__(256, MODE == 1 ? 2 : 3) void k_w4a8(const uint8_t* 
             const_cast<void*>(S), (short)0, (int)((size_t)N * G * SB), 0x00020000);
         const int base = rb * BR * G * SB;
 #pragma unroll
-        for (int c = 0; c < SCH; ++c) {
-            const int ch = tid + 256 * c;
+        for (int c = 0; c < SCHB; ++c) {
+            const int ch = tid + NTB * c;
             if (ch < nch) sv[c] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, base + 16 * ch, 0, 0));
         }
     }
@@ -164,7 +201,7 @@ __global__ __launch_bounds__(256, MODE == 1 ? 2 : 3) void k_w4a8(const uint8_t* 
     // PD register sets, the loop unrolled by PD so each set is a fixed set of
     // registers.  Set i: W[i] holds the weights of the stage it serves; A[i] its
     // activations, written to LDS at the end of the previous stage.
-    u32x4 Wr[PD][RT * LW], Ar[PD][2];
+    u32x4 Wr[PD][RT * LW], Ar[PD][CPT];
 #pragma unroll
     for (int i = 0; i < PD; ++i) {
         ldw(Wr[i], i);
@@ -172,15 +209,15 @@ __global__ __launch_bounds__(256, MODE == 1 ? 2 : 3) void k_w4a8(const uint8_t* 
     }
     if constexpr (MODE == 2) {
 #pragma unroll
-        for (int c = 0; c < SCH; ++c) {
-            const int ch = tid + 256 * c;
+        for (int c = 0; c < SCHB; ++c) {
+            const int ch = tid + NTB * c;
             if (ch < nch) {
                 int row = ch * EPC / G, g = ch * EPC % G;  // walked forward: one division per chunk
 #pragma unroll
                 for (int e = 0; e < EPC; ++e) {
                     const uint32_t wd = sv[c][SK == ScaleKind::F16 ? e / 2 : e];
                     const uint32_t raw = SK == ScaleKind::F16 ? (wd >> (16 * (e & 1))) & 0xFFFFu : wd;
-                    ssT[g * BR + row] = scale_from_raw<SK>(raw);
+                    ssT[g * BR + row] = X16 ? scale_from_raw<SK>(raw) * 0.0625f : scale_from_raw<SK>(raw);
                     if (++g == G) {
                         g = 0;
                         ++row;
@@ -192,7 +229,20 @@ __global__ __launch_bounds__(256, MODE == 1 ? 2 : 3) void k_w4a8(const uint8_t* 
     sta(0, Ar[0]);
     __syncthreads();
 
-    auto stage = [&](int st, u32x4 (&wc)[RT * LW], u32x4 (&ac)[2], const u32x4 (&an)[2]) {
+    i32x4 pb[DEFER ? PD : 1][RT][4];
+    auto scale_into = [&](const i32x4 (&pp)[RT][4], int g) {
+        f32x4 sg[RT];
+#pragma unroll
+        for (int f = 0; f < RT; ++f) sg[f] = *reinterpret_cast<const f32x4*>(&ssT[g * BR + wv * 16 * RT + 16 * f + 4 * q]);
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+            for (int f = 0; f < RT; ++f)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) facc[f][t][r] = fmaf((float)pp[f][t][r], sg[f][r], facc[f][t][r]);
+    };
+    auto stage = [&](int st, u32x4 (&wc)[RT * LW], u32x4 (&ac)[CPT], const u32x4 (&an)[CPT], auto IDX) {
+        constexpr int si = decltype(IDX)::value;  // the stage's slot in the unrolled group of PD
         const int buf = st & 1;
         const int k0 = st * GK;
         const bool gstart = ONEG || k0 % gs == 0, gend = ONEG || (k0 + GK) % gs == 0;
@@ -203,7 +253,10 @@ __global__ __launch_bounds__(256, MODE == 1 ? 2 : 3) void k_w4a8(const uint8_t* 
             if constexpr (WB == 4) {
                 const uint32_t ww[4] = {wc[f].x, wc[f].y, wc[f].z, wc[f].w};
 #pragma unroll
-                for (int i = 0; i < 4; ++i) unpack_i4_to_i8(ww[i], tc, b8[f][2 * i], b8[f][2 * i + 1]);
+                for (int i = 0; i < 4; ++i) {
+                    if constexpr (X16) unpack_i4_to_i8x16(ww[i], xm, b8[f][2 * i], b8[f][2 * i + 1]);
+                    else unpack_i4_to_i8(ww[i], tc, b8[f][2 * i], b8[f][2 * i + 1]);
+                }
             } else {
                 const u32x4 w0 = wc[2 * f], w1 = wc[2 * f + 1];
                 const uint32_t ww[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
@@ -223,12 +276,12 @@ __global__ __launch_bounds__(256, MODE == 1 ? 2 : 3) void k_w4a8(const uint8_t* 
             bk[t][1] = *reinterpret_cast<const i32x4*>(arow + 16);
         }
         f32x4 sc[RT];
-        if constexpr (MODE == 2) {
+        if constexpr (MODE == 2 && !DEFER) {
             // scales of this lane's D rows 16 f + 4 q + r for the group
 #pragma unroll
             for (int f = 0; f < RT; ++f) sc[f] = *reinterpret_cast<const f32x4*>(&ssT[g * BR + wv * 16 * RT + 16 * f + 4 * q]);
         }
-        i32x4 p[RT][4];
+        i32x4 (&p)[RT][4] = pb[DEFER ? si : 0];
 #pragma unroll
         for (int t = 0; t < 4; ++t)
 #pragma unroll
@@ -243,6 +296,9 @@ __global__ __launch_bounds__(256, MODE == 1 ? 2 : 3) void k_w4a8(const uint8_t* 
                                           (int)b8[f][4 * ks + 3]};
                     p[f][t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, bk[t][ks], p[f][t], 0, 0, 0);
                 }
+        if constexpr (DEFER) {
+            if (st > 0) scale_into(pb[(si + PD - 1) % PD], g - 1);
+        }
 #pragma unroll
         for (int t = 0; t < 4; ++t)
 #pragma unroll
@@ -258,7 +314,7 @@ __global__ __launch_bounds__(256, MODE == 1 ? 2 : 3) void k_w4a8(const uint8_t* 
                             if (n < N) reinterpret_cast<int32_t*>(Y)[((size_t)m * N + n) * G + g] = p[f][t][r];
                         }
                     }
-                } else if constexpr (MODE == 2) {
+                } else if constexpr (MODE == 2 && !DEFER) {
                     if (gend) {
 #pragma unroll
                         for (int r = 0; r < 4; ++r) facc[f][t][r] = fmaf((float)p[f][t][r], sc[f][r], facc[f][t][r]);
@@ -269,14 +325,24 @@ __global__ __launch_bounds__(256, MODE == 1 ? 2 : 3) void k_w4a8(const uint8_t* 
         __syncthreads();
     };
 
+    static_assert(PD == 3, "the unrolled stage group below is written out for PD = 3");
+    using I0 = std::integral_constant<int, 0>;
+    using I1 = std::integral_constant<int, 1>;
+    using I2 = std::integral_constant<int, 2>;
     int st = 0;
     for (; st + PD <= nst; st += PD) {
-#pragma unroll
-        for (int i = 0; i < PD; ++i) stage(st + i, Wr[i], Ar[i], Ar[(i + 1) % PD]);
+        stage(st, Wr[0], Ar[0], Ar[1], I0{});
+        stage(st + 1, Wr[1], Ar[1], Ar[2], I1{});
+        stage(st + 2, Wr[2], Ar[2], Ar[0], I2{});
     }
-#pragma unroll
-    for (int i = 0; i < PD; ++i)
-        if (st + i < nst) stage(st + i, Wr[i], Ar[i], Ar[(i + 1) % PD]);
+    if (st < nst) stage(st, Wr[0], Ar[0], Ar[1], I0{});
+    if (st + 1 < nst) stage(st + 1, Wr[1], Ar[1], Ar[2], I1{});
+    if constexpr (DEFER) {  // the last stage's scaling
+        const int last = (nst - 1) % PD;
+        if (last == 0) scale_into(pb[0], nst - 1);
+        else if (last == 1) scale_into(pb[1], nst - 1);
+        else scale_into(pb[DEFER ? 2 : 0], nst - 1);
+    }
 
     if constexpr (MODE != 1) {
         const bool vec_n = vec_y != 0;  // N % 4 == 0 and Y 16-byte aligned
@@ -321,40 +387,60 @@ bool w4a8_supported(const QArgs& a) {
     if (a.k % GK != 0 || a.group_size % GK != 0) return false;
     // byte offsets of the buffer loads are 31-bit
     const size_t lim = (size_t)1 << 31;
-    if ((size_t)(a.n_out + BR) * a.k / 8 * a.wbits >= lim || (size_t)(a.m + BT) * a.k >= lim) return false;
-    if ((size_t)(a.n_out + BR) * (a.k / a.group_size) * 16 >= lim) return false;
+    constexpr int BRMAX = 16 * RT * 12;  // rows of the largest block
+    if ((size_t)(a.n_out + BRMAX) * a.k / 8 * a.wbits >= lim || (size_t)(a.m + BT) * a.k >= lim) return false;
+    if ((size_t)(a.n_out + BRMAX) * (a.k / a.group_size) * 16 >= lim) return false;
     if (a.y_kind == YKind::I32) return true;  // raw sums or per-group partials: no scales used
     // scaled output: the block's scales are staged in LDS (at most GMAX groups per row)
     const int G = a.k / a.group_size;
     const int sb = a.scale_kind == ScaleKind::F16 ? 2 : a.scale_kind == ScaleKind::GroupScale ? 16 : 4;
-    return a.scale_kind != ScaleKind::None && a.xs != nullptr && G <= GMAX && BR * G * sb <= 256 * 16 * SCH;
+    return a.scale_kind != ScaleKind::None && a.xs != nullptr && G <= GMAX && BRMAX * G * sb <= 256 * 16 * SCH;
 }
 
-template <int WB, int MODE, bool ONEG, ScaleKind SK, YKind YK>
+template <int WB, int MODE, bool ONEG, ScaleKind SK, YKind YK, int NWB = 4, bool DEF = false>
 static void launch_g(const QArgs& a, hipStream_t s) {
-    const int nrb = (a.n_out + BR - 1) / BR, ntb = (a.m + BT - 1) / BT;
+    constexpr int BRB = 16 * RT * NWB;
+    const int nrb = (a.n_out + BRB - 1) / BRB, ntb = (a.m + BT - 1) / BT;
     const int nrb8 = (nrb + NXCD - 1) / NXCD * NXCD;  // row blocks padded to whole XCD rounds
-    const dim3 grid(nrb8 * ntb), block(256);
+    const dim3 grid(nrb8 * ntb), block(64 * NWB);
     // two's complement nibbles become offset-binary with a xor of 8 per nibble
     const uint32_t tc = a.xor_mask ? 0x08080808u : 0u;
-    const size_t smem = MODE == 2 ? (size_t)BR * (a.k / a.group_size) * sizeof(float) : 0;
+    const size_t smem = MODE == 2 ? (size_t)BRB * (a.k / a.group_size) * sizeof(float) : 0;
     if (smem > 48 * 1024) {
         static bool raised = false;  // once per instantiation
         if (!raised) {
-            (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&k_w4a8<WB, MODE, ONEG, SK, YK>),
-                                      hipFuncAttributeMaxDynamicSharedMemorySize, BR * GMAX * (int)sizeof(float));
+            (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&k_w4a8<WB, MODE, ONEG, SK, YK, NWB, DEF>),
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, BRB * GMAX * (int)sizeof(float));
             raised = true;
         }
     }
-    hipLaunchKernelGGL((k_w4a8<WB, MODE, ONEG, SK, YK>), grid, block, smem, s, reinterpret_cast<const uint8_t*>(a.w),
+    hipLaunchKernelGGL((k_w4a8<WB, MODE, ONEG, SK, YK, NWB, DEF>), grid, block, smem, s, reinterpret_cast<const uint8_t*>(a.w),
                        a.s, reinterpret_cast<const int8_t*>(a.x), a.xs, a.y, a.m, a.n_out, a.k,
                        a.group_size, tc, nrb, ntb,
                        (a.n_out % 4 == 0 && ((uintptr_t)a.y & 15u) == 0) ? 1 : 0);
 }
 
+// Block shape of the scaled g128 int4 kernel with fp16 scales.  4 waves (64 rows) let up
+// to three blocks share a CU; 11 waves (176 rows, one block per CU, the group scaling
+// deferred by a stage) read the activations a third as often and the weights as often.
+// The wide block is taken when it needs no more wave rounds per SIMD: blocks of 11 waves
+// put up to 3 waves on a SIMD per block, blocks of 4 waves one.  Config 5 (11008 rows, 256
+// tokens): 688 blocks (3 per CU) or 252 blocks (1 per CU): 24.5 against 26.0 us.
+static bool w4a8_wide(const QArgs& a) {
+    const int cus = device_cus(), ntb = (a.m + BT - 1) / BT;
+    const long b4 = (long)(a.n_out + 63) / 64 * ntb, b11 = (long)(a.n_out + 175) / 176 * ntb;
+    const long per_simd4 = (b4 + cus - 1) / cus, per_simd11 = 3 * ((b11 + cus - 1) / cus);
+    return per_simd11 <= per_simd4;
+}
+
 template <int WB, int MODE, ScaleKind SK, YKind YK>
 static void launch_t(const QArgs& a, hipStream_t s) {
-    if (MODE != 0 && a.group_size == GK) return launch_g<WB, MODE, true, SK, YK>(a, s);
+    if (MODE != 0 && a.group_size == GK) {
+        if constexpr (WB == 4 && MODE == 2 && SK == ScaleKind::F16) {
+            if (w4a8_wide(a)) return launch_g<WB, MODE, true, SK, YK, 11, true>(a, s);
+        }
+        return launch_g<WB, MODE, true, SK, YK>(a, s);
+    }
     return launch_g<WB, MODE, false, SK, YK>(a, s);
 }
 

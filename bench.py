@@ -265,7 +265,8 @@ def bench_w8a8(torch, W, ctx, steps, warmup):
     return {"us_per_launch": round(per * 1e6, 2), "value": round(tops, 2), "unit": "TOP/s",
             "hbm_gbs": round(nbytes / per / 1e9, 2),
             "roofline": {"bound": "mfma", "achieved": round(tops, 2), "peak": INT8_MFMA_PEAK_TOPS,
-                         "unit": "TOP/s", "frac": round(tops / INT8_MFMA_PEAK_TOPS, 4), "traffic": None}}
+                         "unit": "TOP/s", "frac": round(tops / INT8_MFMA_PEAK_TOPS, 4),
+                         "traffic": measured_traffic("w8a8")}}
 
 
 QW_BYTES = 14336 * 4096 * 4 + 14336 * 4096 // 2 + 14336 * (4096 // 32) * 2  # read f32, write int4 + f16 scales
@@ -475,7 +476,8 @@ def bench_ffn(torch, W, ctx, steps, warmup):
     return {"us_per_step": round(per * 1e6, 2), "value": round(gbs, 2), "unit": "GB/s",
             "workload": f"hidden {h}, intermediate {i}, int4 g{gs} fp16 scales, m = 1",
             "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS,
-                         "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None}}
+                         "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
+                         "traffic": measured_traffic("ffn")}}
 
 
 def bench_c5_fp(torch, W, ctx, steps, warmup):

@@ -106,6 +106,7 @@ __global__ __launch_bounds__(64 * NWB, NWB == 4 ? (MODE == 1 ? 2 : 3) : 1) void 
     extern __shared__ __attribute__((aligned(16))) float ssT[];  // MODE 2: [G][BR] scales
 
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int wvu = __builtin_amdgcn_readfirstlane(wv);  // the same, as a wave-uniform value
     const int b = blockIdx.x, j = b / NXCD;
     const int rb = (j / ntb) * NXCD + b % NXCD, tbk = j % ntb;
     if (rb >= nrb) return;  // whole block: no barrier is skipped by part of it
@@ -156,7 +157,7 @@ __global__ __launch_bounds__(64 * NWB, NWB == 4 ? (MODE == 1 ? 2 : 3) : 1) void 
         const int so = __builtin_amdgcn_readfirstlane(st * GK);
 #pragma unroll
         for (int i = 0; i < CPT; ++i)
-            if (NTB * (i + 1) <= BT * 8 || tid + NTB * i < BT * 8)  // whole waves
+            if (NTB * (i + 1) <= BT * 8 || 64 * wvu + NTB * i < BT * 8)  // whole waves
                 a[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(ra, av[i], so, 0));
     };
     // int4 weights decode to (k0 k2 k4 k6 | k1 k3 k5 k7) per 8 k, so the activations are
@@ -165,7 +166,7 @@ __global__ __launch_bounds__(64 * NWB, NWB == 4 ? (MODE == 1 ? 2 : 3) : 1) void 
 #pragma unroll
         for (int i = 0; i < CPT; ++i) {
             const int c = tid + NTB * i;
-            if (NTB * (i + 1) <= BT * 8 || c < BT * 8)
+            if (NTB * (i + 1) <= BT * 8 || 64 * wvu + NTB * i < BT * 8)
                 *reinterpret_cast<u32x4*>(&as[buf][c >> 3][16 * (c & 7)]) = WB == 4 ? perm16(a[i]) : a[i];
         }
     };

@@ -116,6 +116,28 @@ def timed_graph(torch, ctx, launch, steps: int, warmup: int, settle_s: float = 0
     return e0.elapsed_time(e1) / 1e3
 
 
+def bench_floor(torch, ctx, steps, warmup):
+    """Streaming floor at config 2's size, with a kernel that is not this plugin's: torch's
+    device copy moving C2_BYTES per launch (half read, half written), rotated over copies
+    beyond the 256 MB MALL and timed like every leg; and the same copy at 512 MiB per
+    launch, where the launch ramp and tail no longer matter.  What the C2 GEMV's HBM rate
+    is compared against (`--only floor`; not in the default run)."""
+    out = {}
+    for label, nb, copies in (("c2_bytes", C2_BYTES // 2, 17), ("512MiB", COPY_BYTES // 2, 2)):
+        src = [torch.empty(nb, dtype=torch.uint8, device="cuda").random_(0, 255) for _ in range(copies)]
+        dst = [torch.empty_like(t) for t in src]
+
+        def launch(i):
+            dst[i % copies].copy_(src[i % copies])
+
+        n = max(3, min(steps, 100))
+        per = timed_graph(torch, ctx, launch, n, max(1, warmup // 4)) / n
+        out[label] = {"bytes_per_launch": 2 * nb, "us_per_launch": round(per * 1e6, 2),
+                      "gbs": round(2 * nb / per / 1e9, 1), "frac": round(2 * nb / per / 1e9 / HBM_PEAK_GBS, 4)}
+        del src, dst
+    return out
+
+
 def bench_c2(torch, W, ctx, steps, warmup):
     from util import int4_weights
     r = np.random.default_rng(2)
@@ -583,7 +605,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=10.0)
-    ap.add_argument("--only", choices=["c1", "c2", "c3", "c4", "c5", "copy", "quant", "dequant", "gemvb",
+    ap.add_argument("--only", choices=["c1", "c2", "c3", "c4", "c5", "copy", "floor", "quant", "dequant", "gemvb",
                                        "gemvt", "gemvh", "w8a8", "ffn", "gemm"],
                     default=None,
                     help="run one leg only and log its timing (profiling); the JSON line comes "
@@ -615,6 +637,12 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         log(f"  copy {COPY_BYTES} bytes x5 done")
+        return
+    if args.only == "floor":
+        fl = bench_floor(torch, ctx, args.steps, args.warmup)
+        for k, v in fl.items():
+            log(f"  device copy, {v['bytes_per_launch']} bytes moved per launch: {v['us_per_launch']} us, "
+                f"{v['gbs']} GB/s ({100 * v['frac']:.1f} % of 8 TB/s)")
         return
     if args.only == "c1":
         c1 = bench_c1(torch, W, ctx, args.steps, args.warmup)

@@ -256,6 +256,33 @@ def test_w8a8_scaled(ctx, n_out, K, m, gs, sfmt, y):
     compare(got, round_to(ref.astype(np.float32), y), f"W8A8 scaled {n_out}x{K} m{m} g{gs}")
 
 
+@pytest.mark.parametrize("m,y", [(256, "f16"), (250, "f32")])
+def test_w8a8_config5_shape_wide_blocks(ctx, m, y):
+    """W8A8 at config 5's shape with g128 fp16 scales runs in 11-wave blocks with the group
+    scaling a stage late; fp32 scales of the same values run in 4-wave blocks. Same products,
+    same group order: bit-identical outputs, and both match the exact group sums."""
+    r = rng(90 + m)
+    n_out, K, gs = 11008, 4096, 128
+    q, _ = int8_weights(r, n_out, K)
+    s16 = r.uniform(0.001, 0.01, size=(n_out, K // gs)).astype(np.float16)
+    a8, ascale = quantize_rows_int8(r.standard_normal((m, K)).astype(np.float32))
+    ycode, ynp = {"f16": (W.F16, np.float16), "f32": (W.F32, np.float32)}[y]
+    wb, xb, asb = ctx.upload(q), ctx.upload(a8), ctx.upload(ascale)
+    outs = []
+    for sfmt, sbuf in ((W.SCALE_F16, s16), (W.SCALE_F32, s16.astype(np.float32))):
+        yb = ctx.alloc(m * n_out * np.dtype(ynp).itemsize)
+        ctx.qmatmul(W.qdesc(n_out, K, m, 8, gs, 0, sfmt, W.I8, ycode), wb, ctx.upload(sbuf), xb, asb, yb)
+        outs.append(ctx.download(yb, ynp, (m, n_out)))
+    assert np.array_equal(outs[0].view(np.uint8), outs[1].view(np.uint8))
+    # exact group sums in float64 (|P_g| <= 127 * 127 * 128, far inside 2^53)
+    ref = np.zeros((m, n_out))
+    qf, af, sf = q.astype(np.float64), a8.astype(np.float64), s16.astype(np.float64)
+    for g in range(K // gs):
+        ref += (af[:, g * gs:(g + 1) * gs] @ qf[:, g * gs:(g + 1) * gs].T) * sf[None, :, g]
+    ref *= ascale.astype(np.float64)[:, None]
+    compare(outs[0].astype(np.float64), round_to(ref.astype(np.float32), y), f"W8A8 config-5 shape m{m} {y}")
+
+
 def test_w8a8_quantize_x(ctx):
     """QUANTIZE_X with int8 weights: bit-identical to the host-quantized int8 path."""
     r = rng(88)

@@ -120,7 +120,7 @@ __global__ __launch_bounds__(64 * NWB, NWB == 4 ? (MODE == 1 ? 2 : 3) : 1) void 
     // DEFER: the group scaling of stage s runs in stage s + 1, after that stage's MFMAs, so
     // the conversions read results finished a stage earlier; PD partial sets rotate with
     // the unrolled stages (same fma order, same results).
-    constexpr bool DEFER = X16 && DEF;
+    constexpr bool DEFER = MODE == 2 && ONEG && DEF;
     const uint32_t xm = tc ? 0u : 0x80808080u;
 
     // Raw buffer loads: each lane keeps a fixed byte offset (voffset) and the stage
@@ -421,12 +421,13 @@ static void launch_g(const QArgs& a, hipStream_t s) {
                        (a.n_out % 4 == 0 && ((uintptr_t)a.y & 15u) == 0) ? 1 : 0);
 }
 
-// Block shape of the scaled g128 int4 kernel with fp16 scales.  4 waves (64 rows) let up
+// Block shape of the scaled g128 kernel with fp16 scales.  4 waves (64 rows) let up
 // to three blocks share a CU; 11 waves (176 rows, one block per CU, the group scaling
 // deferred by a stage) read the activations a third as often and the weights as often.
 // The wide block is taken when it needs no more wave rounds per SIMD: blocks of 11 waves
 // put up to 3 waves on a SIMD per block, blocks of 4 waves one.  Config 5 (11008 rows, 256
-// tokens): 688 blocks (3 per CU) or 252 blocks (1 per CU): 24.5 against 26.0 us.
+// tokens): 688 blocks (3 per CU) or 252 blocks (1 per CU): 24.5 against 26.0 us with int4
+// weights, 27.9 against 32.8 us with int8 weights.
 static bool w4a8_wide(const QArgs& a) {
     const int cus = device_cus(), ntb = (a.m + BT - 1) / BT;
     const long b4 = (long)(a.n_out + 63) / 64 * ntb, b11 = (long)(a.n_out + 175) / 176 * ntb;
@@ -437,7 +438,7 @@ static bool w4a8_wide(const QArgs& a) {
 template <int WB, int MODE, ScaleKind SK, YKind YK>
 static void launch_t(const QArgs& a, hipStream_t s) {
     if (MODE != 0 && a.group_size == GK) {
-        if constexpr (WB == 4 && MODE == 2 && SK == ScaleKind::F16) {
+        if constexpr (MODE == 2 && SK == ScaleKind::F16) {
             if (w4a8_wide(a)) return launch_g<WB, MODE, true, SK, YK, 11, true>(a, s);
         }
         return launch_g<WB, MODE, true, SK, YK>(a, s);

@@ -138,6 +138,36 @@ def bench_floor(torch, ctx, steps, warmup):
     return out
 
 
+def bench_vendor(torch, steps, warmup):
+    """The vendor library on config 4's shape, for comparison only: torch's plain bf16 GEMM
+    (hipBLASLt) X[2048 x 4096] . W[4096 x 14336] with no quantization, as torch.mm with W
+    stored [K x N] and as F.linear with W stored [N x K] (the weight layout of config 4).
+    Eager launches timed with HIP events on the current stream (each is ~0.2 ms, so the
+    launch gaps are negligible).  `--only vendor`; not in the default run."""
+    import torch.nn.functional as F
+    m, n, k = C4["m"], C4["n_out"], C4["k"]
+    x = torch.randn(m, k, device="cuda", dtype=torch.bfloat16)
+    w_kn = torch.randn(k, n, device="cuda", dtype=torch.bfloat16)
+    w_nk = torch.randn(n, k, device="cuda", dtype=torch.bfloat16)
+    out = {}
+    for label, fn in (("mm_w_kxn", lambda: torch.mm(x, w_kn)), ("linear_w_nxk", lambda: F.linear(x, w_nk))):
+        for _ in range(max(3, warmup)):
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        n_it = max(5, min(steps, 50))
+        e0.record()
+        for _ in range(n_it):
+            fn()
+        e1.record()
+        e1.synchronize()
+        per = e0.elapsed_time(e1) / 1e3 / n_it
+        tf = 2.0 * m * n * k / per / 1e12
+        out[label] = {"us_per_launch": round(per * 1e6, 1), "tflops": round(tf, 1),
+                      "frac": round(tf / MFMA_F16_PEAK_TFLOPS, 4)}
+    return out
+
+
 def bench_c2(torch, W, ctx, steps, warmup):
     from util import int4_weights
     r = np.random.default_rng(2)
@@ -605,7 +635,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=10.0)
-    ap.add_argument("--only", choices=["c1", "c2", "c3", "c4", "c5", "copy", "floor", "quant", "dequant", "gemvb",
+    ap.add_argument("--only", choices=["c1", "c2", "c3", "c4", "c5", "copy", "floor", "vendor", "quant", "dequant", "gemvb",
                                        "gemvt", "gemvh", "w8a8", "ffn", "gemm"],
                     default=None,
                     help="run one leg only and log its timing (profiling); the JSON line comes "
@@ -637,6 +667,12 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         log(f"  copy {COPY_BYTES} bytes x5 done")
+        return
+    if args.only == "vendor":
+        for k, v in bench_vendor(torch, args.steps, args.warmup).items():
+            log(f"  hipBLASLt bf16 {k}: {v['us_per_launch']} us, {v['tflops']} TFLOP/s ({100 * v['frac']:.1f} % of 2.5 PF)")
+        c4 = bench_c4(torch, W, ctx, args.steps, args.warmup)
+        log(f"  C4 {c4['per_launch_s']*1e6:.1f} us/launch, {c4['tflops']:.1f} TFLOP/s")
         return
     if args.only == "floor":
         fl = bench_floor(torch, ctx, args.steps, args.warmup)

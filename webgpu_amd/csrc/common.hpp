@@ -143,6 +143,38 @@ __device__ __forceinline__ float load_x(const void* x, size_t idx) {
     else return (float)reinterpret_cast<const int8_t*>(x)[idx];
 }
 
+// Max / min across the 64 lanes with the DPP pattern of wave_sum (below); rows outside a step's row
+// mask compare a lane with itself, so the operation only needs to be idempotent.  Every
+// lane gets the result (lane 63's, read back as a uniform value).  Replaces six dependent
+// ds_bpermute round trips of a __shfl_xor butterfly.
+template <int CTRL, int ROWMASK>
+__device__ __forceinline__ int dpp_self(int v) {
+    return __builtin_amdgcn_update_dpp(v, v, CTRL, ROWMASK, 0xF, false);
+}
+template <typename Op>
+__device__ __forceinline__ int wave_idem(int v, Op op) {
+    v = op(v, dpp_self<0xB1, 0xF>(v));
+    v = op(v, dpp_self<0x4E, 0xF>(v));
+    v = op(v, dpp_self<0x141, 0xF>(v));
+    v = op(v, dpp_self<0x140, 0xF>(v));
+    v = op(v, dpp_self<0x142, 0xA>(v));
+    v = op(v, dpp_self<0x143, 0xC>(v));
+    return __builtin_amdgcn_readlane(v, 63);
+}
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+    return (uint32_t)wave_idem((int)v, [](int a, int b) { return (int)max((uint32_t)a, (uint32_t)b); });
+}
+__device__ __forceinline__ float wave_max_f32(float v) {
+    return __builtin_bit_cast(float, wave_idem(__builtin_bit_cast(int, v), [](int a, int b) {
+        return __builtin_bit_cast(int, fmaxf(__builtin_bit_cast(float, a), __builtin_bit_cast(float, b)));
+    }));
+}
+__device__ __forceinline__ float wave_min_f32(float v) {
+    return __builtin_bit_cast(float, wave_idem(__builtin_bit_cast(int, v), [](int a, int b) {
+        return __builtin_bit_cast(int, fminf(__builtin_bit_cast(float, a), __builtin_bit_cast(float, b)));
+    }));
+}
+
 // ---- fp16 staging of wide activations ---------------------------------------
 // Kernels that feed bf16 / fp32 activations to fp16 MFMAs scale each activation row by
 // a power of two first: fac = 2^(E - 14) with 2^E <= max|x| < 2^(E+1), so x / fac has
@@ -190,8 +222,7 @@ __device__ __forceinline__ float row_scale_fold(const void* s, size_t row, int G
         mx = max(mx, max(max(scale_abs_bits<K>(a), scale_abs_bits<K>(b)), max(scale_abs_bits<K>(c), scale_abs_bits<K>(d))));
     }
     for (; g < G; g += 64) mx = max(mx, scale_abs_bits<K>(load_scale_raw<K>(s, row * G + g)));
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) mx = max(mx, (uint32_t)__shfl_xor((int)mx, o, 64));
+    mx = wave_max_u32(mx);
     // A NaN scale compares above every finite value and Inf as bits, so it also keeps fold = 1.
     return scale_fold_factor(mx);
 }
@@ -212,8 +243,7 @@ __device__ __forceinline__ u32x4 dequant8_f32s(uint32_t w, float s) {
 
 // Block-wide max of a per-thread value; `red` is __shared__ scratch of >= 16 words.
 __device__ __forceinline__ uint32_t block_max_u32(uint32_t v, uint32_t* red) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = max(v, (uint32_t)__shfl_xor((int)v, o, 64));
+    v = wave_max_u32(v);
     const int wv = threadIdx.x >> 6;
     if ((threadIdx.x & 63) == 0) red[wv] = v;
     __syncthreads();
@@ -243,6 +273,7 @@ __device__ __forceinline__ float wave_sum(float v) {
     v = dpp_add<0x143, 0xC>(v);
     return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
 }
+
 #endif
 
 // ---------------------------------------------------------------------------

@@ -138,8 +138,7 @@ __global__ __launch_bounds__(256) void k_x_to_f16_rows(const void* __restrict__ 
             const u32x4 u = xr[c];
             mx = max(mx, max(max(bf16x2_absmax(u.x), bf16x2_absmax(u.y)), max(bf16x2_absmax(u.z), bf16x2_absmax(u.w))));
         }
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) mx = max(mx, (uint32_t)__shfl_xor((int)mx, o, 64));
+        mx = wave_max_u32(mx);
         const float f = row_pow2_factor(mx, 7);
         const float inv = 1.0f / f;  // exact: f is a power of two
 #pragma unroll
@@ -182,8 +181,7 @@ __global__ __launch_bounds__(512) void k_x_to_f16_frag(const void* __restrict__ 
             }
 #pragma unroll
             for (int r = 0; r < 8; ++r) {
-#pragma unroll
-                for (int o = 32; o > 0; o >>= 1) mx[r] = max(mx[r], (uint32_t)__shfl_xor((int)mx[r], o, 64));
+                mx[r] = wave_max_u32(mx[r]);
                 if (lane == 0 && r < nr) wfold[w0 + r] = scale_fold_factor(mx[r]);
             }
         } else {
@@ -223,8 +221,7 @@ __global__ __launch_bounds__(512) void k_x_to_f16_frag(const void* __restrict__ 
                 mx = max(mx, max(max(bf16x2_absmax(u.x), bf16x2_absmax(u.y)),
                                  max(bf16x2_absmax(u.z), bf16x2_absmax(u.w))));
             }
-#pragma unroll
-            for (int o = 32; o > 0; o >>= 1) mx = max(mx, (uint32_t)__shfl_xor((int)mx, o, 64));
+            mx = wave_max_u32(mx);
             const float f = row_pow2_factor(mx, 7);
             const float inv = 1.0f / f;  // exact: f is a power of two
 #pragma unroll

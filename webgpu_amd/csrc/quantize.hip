@@ -192,11 +192,8 @@ __global__ __launch_bounds__(256) void k_quantize_large(const void* __restrict__
             mn = fminf(mn, v[i]);
         }
     }
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-        mx = fmaxf(mx, __shfl_xor(mx, o, 64));
-        mn = fminf(mn, __shfl_xor(mn, o, 64));
-    }
+    mx = wave_max_f32(mx);
+    mn = wave_min_f32(mn);
     const float s = group_scale<BITS>(mx, mn);
     const float sq = stored_scale<SK>(s);
     if (lane == 0) store_scale<SK>(S, g, s, mn, mx);
@@ -235,11 +232,8 @@ __global__ __launch_bounds__(NT) void k_quantize_rows(const void* __restrict__ X
             }
         }
     }
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-        mx = fmaxf(mx, __shfl_xor(mx, o, 64));
-        mn = fminf(mn, __shfl_xor(mn, o, 64));
-    }
+    mx = wave_max_f32(mx);
+    mn = wave_min_f32(mn);
     if ((tid & 63) == 0) {
         red[0][tid >> 6] = mx;
         red[1][tid >> 6] = mn;

@@ -348,7 +348,8 @@ __global__ __launch_bounds__(64 * MAXW) void k_qgemm_small(
 //     R_PD chunks ahead; 16-byte unit b of tile row r sits at unit b ^ r of the row, so the
 //     fragment reads (16 rows of one unit) hit 16 distinct bank groups;
 //   - X goes global -> LDS the same way in super-chunks of R_SKC k (all rows of the
-//     m-tiles, double-buffered): the block meets at a barrier once per super-chunk;
+//     m-tiles, or 8 rows for m <= 8, double-buffered): the block meets at a barrier once
+//     per super-chunk;
 //   - int8 -> fp16 is exact and in natural k order: v_cvt_f16_i16 with SDWA reads a
 //     sign-extended byte and writes one half of the register, 4 VALU per 4 weights.
 //   - Lane (row r16, quarter kq) feeds k = 64 l + 16 kq + 8 st + 0..7 of a chunk to k-step

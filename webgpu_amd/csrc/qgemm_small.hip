@@ -348,17 +348,14 @@ __global__ __launch_bounds__(64 * MAXW) void k_qgemm_small(
 //     R_PD chunks ahead; 16-byte unit b of tile row r sits at unit b ^ r of the row, so the
 //     fragment reads (16 rows of one unit) hit 16 distinct bank groups;
 //   - X goes global -> LDS the same way in super-chunks of R_SKC k (all rows of the
-//     m-tiles, or 8 rows for m <= 8, double-buffered): the block meets at a barrier once
-//     per super-chunk;
+//     m-tiles, double-buffered): the block meets at a barrier once per super-chunk;
 //   - int8 -> fp16 is exact and in natural k order: v_cvt_f16_i16 with SDWA reads a
 //     sign-extended byte and writes one half of the register, 4 VALU per 4 weights.
 //   - Lane (row r16, quarter kq) feeds k = 64 l + 16 kq + 8 st + 0..7 of a chunk to k-step
 //     (l, st); the X fragment of token t is the same 16 bytes of X row t.
 // A wave waits only for its own loads (s_waitcnt); the barrier publishes X.
 namespace {
-// weight chunks (256 k) in flight per wave: 3, or 4 when X stages only 8 token rows (m <= 8;
-// the X buffers then take half the LDS and the fourth ring slot fits beside 7 rings)
-constexpr int r_pd(int xr) { return xr < 16 ? 4 : 3; }
+constexpr int R_PD = 3;      // weight chunks (256 k) in flight per wave
 constexpr int R_XJ = 8;      // X loads per wave per super-chunk (<= 32 jobs, >= 4 waves)
 // k per X super-chunk: 1024 with one m-tile, 512 with two (the double-buffered X then fits
 // beside 7 weight rings)
@@ -390,39 +387,21 @@ constexpr int r_vmcnt(int n) { return (n & 0xF) | ((n >> 4) << 14) | (0x7 << 4) 
 template <int N>
 __device__ __forceinline__ void wait_vm() { __builtin_amdgcn_s_waitcnt(r_vmcnt(N)); }
 
-// xr: token rows staged per X buffer (8 for m <= 8, else 16 mt)
-size_t i8row_lds(int xr, int mt, int nw) { return (size_t)2 * xr * r_xp(mt) + (size_t)nw * r_pd(xr) * 4096 + 1024; }
-
-// vmcnt that leaves weight chunk c complete at chunk slot p of a super-chunk: the loads a
-// wave issues after W(c), which went out in chunk c - pd (each chunk refills W(c + pd), 4
-// loads, and slot 0 then issues the next super-chunk's R_XJ X loads).
-constexpr int r_wait(int p, int pd, int cps) {
-    int n = 0;
-    for (int d = pd; d >= 1; --d) {
-        const int pp = ((p - d) % cps + cps) % cps;
-        if (d < pd) n += 4;
-        if (pp == 0) n += R_XJ;
-    }
-    return n;
-}
-static_assert(r_wait(0, 3, 4) == 8 && r_wait(1, 3, 4) == 16 && r_wait(3, 3, 4) == 16 && r_wait(1, 3, 2) == 24,
-              "wait counts of the three-slot ring");
+size_t i8row_lds(int mt, int nw) { return (size_t)2 * 16 * mt * r_xp(mt) + (size_t)nw * R_PD * 4096 + 1024; }
 }  // namespace
 
-template <int MT, ScaleKind SK, YKind YK, int XR = 16 * MT>
+template <int MT, ScaleKind SK, YKind YK>
 __global__ __launch_bounds__(64 * MAXW) void k_qgemm_i8row(const uint8_t* __restrict__ W, const void* __restrict__ S,
                                                          const f16* __restrict__ X, void* __restrict__ Y, int M, int N,
                                                          int K, EpiArgs epi) {
-    // LDS: X [2][XR][R_XP] | weight rings [nw][R_PD][16 rows x 256 B] | spare 1 KB
+    // LDS: X [2][16 MT][R_XP] | weight rings [nw][R_PD][16 rows x 256 B] | spare 1 KB
     extern __shared__ __attribute__((aligned(16))) uint8_t xl[];
     const int nw = blockDim.x >> 6;
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int n0 = (blockIdx.x * nw + wv) * 16;
     const int r16 = lane & 15, kq = lane >> 4;
     constexpr int R_SKC = r_skc(MT), R_XP = r_xp(MT), CPS = R_SKC / 256;
-    constexpr int XB = XR * R_XP;  // bytes per X buffer
-    constexpr int R_PD = r_pd(XR);
-    static_assert(XR == 16 * MT || (MT == 1 && XR == 8), "staged token rows");
+    constexpr int XB = 16 * MT * R_XP;  // bytes per X buffer
     uint8_t* ring = xl + 2 * XB + wv * (R_PD * 4096);
     uint8_t* spare = xl + 2 * XB + nw * (R_PD * 4096);
     const int nchunks = K / 256, nsc = K / R_SKC;
@@ -478,12 +457,15 @@ __global__ __launch_bounds__(64 * MAXW) void k_qgemm_i8row(const uint8_t* __rest
     for (int i = 0; i < R_PD; ++i) load_w(i);
 
     // Issue order per super-chunk: chunk p = 0 refills W(c + R_PD) then X(sc + 1); chunks
-    // 1 .. CPS-1 refill W(c + R_PD).  The prologue (X(0), W(0 .. R_PD - 1)) issues at least
-    // as many weight loads after X(0), so the counts below hold from the start:
+    // 1 .. CPS-1 refill W(c + R_PD).  The prologue (X(0), W(0..2)) has the same shape, so
+    // the counts below hold from the start:
     //   - at the barrier, X(sc) is complete once the weight loads issued after it may
-    //     remain: W(c+1 .. c+CPS-1), 4 (CPS - 1) loads;
-    //   - chunk c's weights: r_wait(p) (at p = 0 the smaller of it and the barrier's count).
-    constexpr int WB_BAR = 4 * (CPS - 1);
+    //     remain: CPS == 4: W(c+1 .. c+3) = 12 loads; CPS == 2: W(c+2) = 4 (the barrier then
+    //     also completes W(c), W(c+1));
+    //   - chunk c's weights: the loads issued after W(c) (4 per chunk, R_XJ for an X
+    //     super-chunk): CPS == 4: 8 at p = 0 and 16 at p = 1..3; CPS == 2: covered by the
+    //     barrier at p = 0, 24 at p = 1.
+    constexpr int WB_BAR = CPS == 4 ? 12 : 4;
     const int wrd = r16 * 256;  // this lane's row in a ring slot
     for (int sc = 0; sc < nsc; ++sc) {
         // the barrier publishes every wave's share of X(sc) and retires the other X buffer
@@ -494,10 +476,13 @@ __global__ __launch_bounds__(64 * MAXW) void k_qgemm_i8row(const uint8_t* __rest
 #pragma unroll
         for (int p = 0; p < CPS; ++p) {
             const int c = CPS * sc + p;
-            if (p == 0) wait_vm<(r_wait(0, R_PD, CPS) < WB_BAR ? r_wait(0, R_PD, CPS) : WB_BAR)>();
-            else if (p == 1) wait_vm<r_wait(1, R_PD, CPS)>();
-            else if (p == 2) wait_vm<r_wait(2, R_PD, CPS)>();
-            else wait_vm<r_wait(3, R_PD, CPS)>();
+            if (CPS == 4) {
+                if (p == 0) wait_vm<8>();
+                else wait_vm<16>();
+            } else {
+                if (p == 0) wait_vm<WB_BAR>();
+                else wait_vm<24>();
+            }
             const uint8_t* slot = ring + (c % R_PD) * 4096 + wrd;
             u32x4 q[4];
 #pragma unroll
@@ -521,8 +506,7 @@ __global__ __launch_bounds__(64 * MAXW) void k_qgemm_i8row(const uint8_t* __rest
 #pragma unroll
                     for (int t = 0; t < MT; ++t) {
                         const f16x8 bx =
-                            *reinterpret_cast<const f16x8*>(xb + (XR < 16 ? (r16 & (XR - 1)) : 16 * t + r16) * R_XP +
-                                                            2 * (64 * l + 16 * kq + 8 * st));
+                            *reinterpret_cast<const f16x8*>(xb + (16 * t + r16) * R_XP + 2 * (64 * l + 16 * kq + 8 * st));
                         acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[l][st], bx, acc[t], 0, 0, 0);
                     }
         }
@@ -554,7 +538,7 @@ static bool i8row_ok(const QArgs& a) {
            ((uintptr_t)a.x & 15u) == 0 && ((uintptr_t)a.w & 15u) == 0;
 }
 
-template <int MT, ScaleKind SK, YKind YK, int XR = 16 * MT>
+template <int MT, ScaleKind SK, YKind YK>
 static void launch_i8row(const QArgs& a, hipStream_t s) {
     const int cus = device_cus();
     const int tiles = (a.n_out + 15) / 16;
@@ -562,22 +546,21 @@ static void launch_i8row(const QArgs& a, hipStream_t s) {
     if (tiles % cus == 0 && tiles / cus <= MAXW) nw = tiles / cus;
     else if (tiles <= cus * MAXW && tiles >= cus) nw = (tiles + cus - 1) / cus;
     nw = std::max(4, std::min(nw, MAXW));  // >= 4: the X loads of a super-chunk fit R_XJ per wave
-    while (i8row_lds(XR, MT, nw) > 160 * 1024) --nw;
+    while (i8row_lds(MT, nw) > 160 * 1024) --nw;
     static bool attr = [] {
-        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&k_qgemm_i8row<MT, SK, YK, XR>),
+        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&k_qgemm_i8row<MT, SK, YK>),
                                   hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
         return true;
     }();
     (void)attr;
-    hipLaunchKernelGGL((k_qgemm_i8row<MT, SK, YK, XR>), dim3((tiles + nw - 1) / nw), dim3(64 * nw), i8row_lds(XR, MT, nw), s,
+    hipLaunchKernelGGL((k_qgemm_i8row<MT, SK, YK>), dim3((tiles + nw - 1) / nw), dim3(64 * nw), i8row_lds(MT, nw), s,
                        reinterpret_cast<const uint8_t*>(a.w), a.s, reinterpret_cast<const f16*>(a.x), a.y, a.m,
                        a.n_out, a.k, a.epi);
 }
 
 template <ScaleKind SK, YKind YK>
 static void launch_i8row_m(const QArgs& a, hipStream_t s) {
-    if (a.m <= 8) launch_i8row<1, SK, YK, 8>(a, s);
-    else if (a.m <= 16) launch_i8row<1, SK, YK>(a, s);
+    if (a.m <= 16) launch_i8row<1, SK, YK>(a, s);
     else launch_i8row<2, SK, YK>(a, s);
 }
 

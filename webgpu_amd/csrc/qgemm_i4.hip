@@ -27,8 +27,8 @@
 // double-buffered LDS (2 x 72 KB): while the MFMAs of stage s run, the global loads
 // of stage s+1 are in flight; W is dequantised and both tiles are written to the
 // other buffer before one barrier per stage.  X is restaged to fp16 once per call
-// by a pre-pass.  For k <= 8192 the default is k_qgemm_i4_xr (below): the same block
-// tile with X read from a fragment-ordered staging straight into registers and only the
+// by a pre-pass.  For k <= 8192 the default is k_qgemm_i4_xr (below): 512 x 128 block
+// tiles with X read from a fragment-ordered staging straight into registers and only the
 // weights in LDS; LUX_HIP_C4_STAGED=1 selects the kernel described here.
 #include <algorithm>
 #include <cstdlib>
@@ -463,10 +463,13 @@ void k_qgemm_i4_large(const f16* __restrict__ X, const float* __restrict__ xfac,
 
 // The same GEMM with the activation operand read straight from X staged in fragment
 // order (k_x_to_f16_frag) into MFMA registers, one contiguous 1 KB per fragment, so only
-// the dequantised weights pass through LDS.  8 waves in a 4 (m) x 2 (n) grid, each with
-// TM x TN tiles of 32 x 32: TM = 2, TN = 4 gives a 256 x 256 block tile, TM = 4, TN = 2 a
-// 512 x 128 one (each weight tile dequantised once per 512 rows of X, half as often, for
-// twice the X fragment loads).  The MFMA sequence per output element is the staged
+// the dequantised weights pass through LDS.  8 waves in a WGM (m) x 8 / WGM (n) grid, each
+// with TM x TN tiles of 32 x 32.  The launcher uses WGM = 8, TM = 2, TN = 4: a 512 x 128
+// block tile (each weight tile dequantised once per 512 rows of X) whose waves are
+// stacked in m, 64 x 128 each, so every wave loads X fragments no other wave of the
+// block needs and all eight read the weight tile from LDS.  With the waves in a 4 x 2
+// grid (TM = 4, TN = 2) the two n-waves load the same X fragments, which doubles the
+// vector-memory requests for X.  The MFMA sequence per output element is the staged
 // kernel's, so the results are identical.
 template <ScaleKind SK, YKind YK, int TM, int TN, int WGM = 4>
 __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2)))
@@ -740,7 +743,7 @@ static void launch_t(const QArgs& a, const f16* xst, const float* xfac, const fl
     if (xr) {  // 512 x 128 block tiles
         const dim3 xgrid(sm ? (ny + 63) / 64 : (a.n_out + 127) / 128, (a.m + 511) / 512);
         const size_t lds = (size_t)2 * 128 * LDS_ROW * sizeof(f16);
-        hipLaunchKernelGGL((k_qgemm_i4_xr<SK, YK, 4, 2>), xgrid, block, lds, s, xst, xfac,
+        hipLaunchKernelGGL((k_qgemm_i4_xr<SK, YK, 2, 4, 8>), xgrid, block, lds, s, xst, xfac,
                            reinterpret_cast<const uint32_t*>(a.w), a.s, wfold, a.y, a.m, a.n_out, a.k,
                            a.group_size, a.xor_mask, vy, a.epi);
         return;

@@ -87,6 +87,10 @@ __device__ __forceinline__ float bf16_bits_to_f32(uint32_t b) {
     return __builtin_bit_cast(float, b << 16);
 }
 
+// Cache-policy operand of the buffer-load builtins for data read once (streamed weights):
+// the nt bit, which __builtin_nontemporal_load sets on global loads.
+constexpr int kNontemporal = 2;
+
 // bfloat16 round-to-nearest-even (NaN kept quiet): the hardware conversion
 // (v_cvt_pk_bf16_f32 on gfx950), the same one store_y4 uses.
 __device__ __forceinline__ uint16_t f32_to_bf16_bits(float v) { return __builtin_bit_cast(uint16_t, (__bf16)v); }

@@ -445,7 +445,7 @@ __global__ __launch_bounds__(64 * MAXW) void k_qgemm_i8row(const uint8_t* __rest
 #pragma unroll
         for (int j = 0; j < 4; ++j)
             __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (__attribute__((address_space(3))) void*)(slot + 1024 * j), 16,
-                                                     woff[j], so, 0, 0);
+                                                     woff[j], so, 0, kNontemporal);
     };
 
     f32x4 acc[MT];

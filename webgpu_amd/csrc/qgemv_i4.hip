@@ -126,7 +126,8 @@ __global__ __launch_bounds__(256) void k_qgemv_i4_f16(const u32x4* __restrict__ 
         for (int j = 0; j < SPL; ++j) {
             q[r][j] = __builtin_nontemporal_load(W + row * s_row + sl[j]);
             if constexpr (SK == ScaleKind::F16)  // aligned u32 holding this scale (g_row is even)
-                sraw[r][j] = reinterpret_cast<const uint32_t*>(S)[(row * g_row + (sl[j] >> spg_shift)) >> 1];
+                sraw[r][j] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(S) +
+                                                        ((row * g_row + (sl[j] >> spg_shift)) >> 1));
             else
                 sraw[r][j] = load_scale_raw<SK>(S, row * g_row + (sl[j] >> spg_shift));
         }

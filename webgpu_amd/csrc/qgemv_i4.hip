@@ -277,8 +277,8 @@ static void launch_rwd(const QArgs& a, hipStream_t s) {
 }
 
 // Two rows of prefetch (issue row r+2, then compute row r) measured best on MI355X for
-// config 2 (6.9 us against 7.0 us with one row); issuing all rows up front bunches the
-// arrivals and lengthens the tail (8.6 us).
+// config 2 (7.0 us against 7.1 us with one row, 7.2 us with three and 7.4 us with four);
+// issuing all rows up front bunches the arrivals and lengthens the tail (8.6 us).
 template <int SPL, int RW, ScaleKind SK, YKind YK, bool RN, int KS = 1>
 static void launch_rw(const QArgs& a, hipStream_t s) {
     launch_rwd<SPL, RW, 2, SK, YK, RN, KS>(a, s);

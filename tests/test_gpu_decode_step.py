@@ -191,7 +191,7 @@ def test_rms_norm_qmatmul_two_launch_routes(ctx, case):
     m, n_out, k, bits, gs, sf, xdt, ydt, flags, epi = 1, 512, 4096, 4, 32, W.SCALE_F16, W.F16, W.F16, 0, W.EPI_NONE
     if case == "small_m":
         m, epi = 5, W.EPI_SILU_MUL
-    elif case == "k16384":
+    elif case == "k16384":  # outside the fused GEMV; the plain GEMV splits k in quarters
         k = 16384
     elif case == "k_halves":  # few long rows: the plain GEMV splits k, so both kernels run
         k = 8192

@@ -57,22 +57,25 @@ def test_int4_gemv_shapes(ctx, n_out, K, gs):
 
 
 @pytest.mark.parametrize("n_out,K,gs,coding,y", [
-    (4096, 14336, 32, 0, "f32"),     # the decode down-projection: four slices per lane per half
-    (4099, 8192, 64, 1, "f16"),      # ragged last block: waves without rows run to the barrier
-    (300, 4096, 32, 0, "bf16"),      # one slice per lane per half
-    (2048, 16384, 128, 1, "f32"),    # the largest k split into halves
-    (1000, 4160, 32, 0, "f32")])     # halves of 65 slices: the second pass of each half ragged
-def test_int4_gemv_k_halves(ctx, n_out, K, gs, coding, y):
-    """Few, long rows: two waves per row, one per half of k, their sums added in LDS."""
+    (4096, 14336, 32, 0, "f32"),     # the decode down-projection: quarters of 112 slices
+    (4099, 8192, 64, 1, "f16"),      # halves; ragged last block: waves without rows run to the barrier
+    (300, 4096, 32, 0, "bf16"),      # halves of one slice per lane
+    (2048, 16384, 128, 1, "f32"),    # the largest k: quarters of two full slices per lane
+    (1000, 4160, 32, 0, "f32"),      # halves of 65 slices: the second pass of each half ragged
+    (1000, 8320, 32, 1, "f32"),      # quarters of 65 slices: the second pass of each quarter ragged
+    (4099, 12288, 64, 0, "f16"),     # quarters, ragged last block
+    (700, 8256, 32, 0, "f32")])      # k > 8192 but not a multiple of 128: halves of 129 slices
+def test_int4_gemv_k_parts(ctx, n_out, K, gs, coding, y):
+    """Few, long rows: two or four waves per row, one per part of k, their sums added in LDS."""
     r = rng(n_out + K + coding)
     q, Wp, s = int4_weights(r, n_out, K, gs, coding)
     x = r.standard_normal(K).astype(np.float16)
     got = _run_gemv(ctx, Wp, s, x, n_out, K, gs, coding=coding, y=y)
     ref = _oracle(Wp, s.astype(np.float32), x.astype(np.float32), gs, coding)
     if y == "f32":
-        compare(got, ref, f"gemv halves {n_out}x{K} g{gs}", rel_tol=1e-5, abs_frac=1e-5)
+        compare(got, ref, f"gemv k parts {n_out}x{K} g{gs}", rel_tol=1e-5, abs_frac=1e-5)
     else:
-        compare(got, round_to(ref, y), f"gemv halves {n_out}x{K} g{gs} {y}")
+        compare(got, round_to(ref, y), f"gemv k parts {n_out}x{K} g{gs} {y}")
 
 
 @pytest.mark.parametrize("scale_fmt", [W.SCALE_F32, W.SCALE_GROUPSCALE])

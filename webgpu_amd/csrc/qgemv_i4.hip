@@ -61,25 +61,26 @@ __device__ __forceinline__ float dot_slice_sub(const uint32_t (&q)[4], const f16
 // / K + eps), with k_rms_norm's arithmetic in k_rms_norm's order (thread t sums elements
 // t + 256 j, j ascending, then the DPP wave sum and the four wave sums in a fixed order),
 // so the staged row is bit-identical to what k_rms_norm would have written.
-// KS = 2 (few, long rows: the decode down-projection): waves w and w + 2 of a block take
-// the same RW rows, w the first half of k and w + 2 the second, so each wave has twice
-// the rows to pipeline; the two halves' sums meet in LDS and are added in that order.
+// KS = 2 or 4 (few, long rows: the decode down-projection): the block's waves w, w + 4/KS,
+// ... take the same RW rows, each one KS-th of k in order, so each wave has KS times the
+// rows to pipeline; the parts' sums meet in LDS and are added in k order.
 template <int SPL, int RW, int D, ScaleKind SK, YKind YK, bool XOR, bool SM, bool RN, int KS = 1>
 __global__ __launch_bounds__(256) void k_qgemv_i4_f16(const u32x4* __restrict__ W,
                                                       const void* __restrict__ S,
                                                       const f16* __restrict__ x,
                                                       void* __restrict__ y, int n_out, int K,
                                                       int spg_shift, uint32_t xor_mask, EpiArgs epi, RnArgs rn) {
-    static_assert(KS == 1 || (KS == 2 && !SM && !RN), "k halves: plain rows only");
+    static_assert(KS == 1 || ((KS == 2 || KS == 4) && !SM && !RN), "k parts: plain rows only");
+    constexpr int RS = 4 / KS;  // row sets per block: wave w takes row set w % RS, k part w / RS
     __shared__ u32x4 xs[KS * SPL * 256];  // K <= KS * SPL * 2048 halves
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int row0 = (KS == 1 ? blockIdx.x * 4 + wave : blockIdx.x * 2 + (wave & 1)) * RW;
+    const int row0 = (blockIdx.x * RS + wave % RS) * RW;
     const bool active = row0 < n_out;
     const int nrows = min(RW, n_out - row0);
     const int s_row = K >> 5;        // slices per row
     const int g_row = s_row >> spg_shift;  // groups per row (slices per group: a power of two)
-    const int s_part = s_row / KS;   // slices of the wave's part of k (KS = 2: s_row is even)
-    const int s_base = KS == 1 ? 0 : (wave >> 1) * s_part;
+    const int s_part = s_row / KS;   // slices of the wave's part of k (s_row is a multiple of KS)
+    const int s_base = (wave / RS) * s_part;
 
     // Load order matters: vmcnt retires loads in issue order, so the block's x chunks
     // (L2 hits) go first, then the first D rows of weight slices and raw scales.  All
@@ -162,7 +163,7 @@ __global__ __launch_bounds__(256) void k_qgemv_i4_f16(const u32x4* __restrict__ 
         }
     }
     __syncthreads();  // every wave of the block reaches this before any returns
-    // KS = 2: waves without rows still run (on clamped rows) to the halves' barrier
+    // KS > 1: waves without rows still run (on clamped rows) to the parts' barrier
     if (KS == 1 && !active) return;
 
     // x pairs in decode order and, per slice, -8 * sum(x) (offset-binary q = n - 8).
@@ -213,12 +214,15 @@ __global__ __launch_bounds__(256) void k_qgemv_i4_f16(const u32x4* __restrict__ 
     if constexpr (SM) {
         const float up = __shfl_down(res, 1, 64);  // the pair's up row sits in the next lane
         if (lane < nrows && !(lane & 1)) store_y<YK>(y, (row0 + lane) >> 1, silu_f(res) * up);
-    } else if constexpr (KS == 2) {
-        __shared__ float hi_half[2][64];
-        if (wave >= 2) hi_half[wave & 1][lane] = res;
+    } else if constexpr (KS > 1) {  // the parts' sums meet in LDS, added in k order
+        __shared__ float part_k[KS - 1][RS][64];
+        const int kp = wave / RS, rs = wave % RS;
+        if (kp > 0) part_k[kp - 1][rs][lane] = res;
         __syncthreads();
-        const float tot = res + hi_half[wave & 1][lane];
-        if (wave < 2 && lane < nrows) store_y<YK>(y, row0 + lane, apply_epi(tot, epi, 0, row0 + lane, n_out));
+        float tot = res;
+#pragma unroll
+        for (int i = 0; i < KS - 1; ++i) tot += part_k[i][rs][lane];
+        if (kp == 0 && lane < nrows) store_y<YK>(y, row0 + lane, apply_epi(tot, epi, 0, row0 + lane, n_out));
     } else {
         if (lane < nrows) store_y<YK>(y, row0 + lane, apply_epi(res, epi, 0, row0 + lane, n_out));
     }
@@ -259,9 +263,9 @@ static void launch_rwd(const QArgs& a, hipStream_t s) {
     auto go = [&](auto kern) {
         hipLaunchKernelGGL(kern, grid, block, 0, s, w, a.s, x, a.y, a.n_out, a.k, shift, a.xor_mask, a.epi, a.rn);
     };
-    if constexpr (KS == 2) {
-        if (a.xor_mask) go(k_qgemv_i4_f16<SPL, RW, D, SK, YK, true, false, false, 2>);
-        else go(k_qgemv_i4_f16<SPL, RW, D, SK, YK, false, false, false, 2>);
+    if constexpr (KS > 1) {
+        if (a.xor_mask) go(k_qgemv_i4_f16<SPL, RW, D, SK, YK, true, false, false, KS>);
+        else go(k_qgemv_i4_f16<SPL, RW, D, SK, YK, false, false, false, KS>);
         return;
     }
     const bool sm = a.epi.kind == (int)Epi::SiluMul;
@@ -306,18 +310,23 @@ static void launch_fast(const QArgs& a, hipStream_t s) {
     }
 }
 
-// Halves of k per row (KS = 2) when rows are few and long: at 8 waves per CU each wave
+// Parts of k per row (KS = 2 or 4) when rows are few and long: at 8 waves per CU each wave
 // would get at most two rows (nothing to overlap its math with), k is at least 4096 and
-// splits into whole slices, and each half fits four slices per lane.  fp16 scales, no
-// gated pairs, no fused rms_norm.
-static bool use_k_halves(const QArgs& a) {
+// splits into whole slices.  Halves while each fits two slices per lane (k <= 8192),
+// quarters above that (two slices per lane up to k = 16384), so a wave keeps the config-2
+// shape of two slices per lane and up to 8 rows.  Measured at 4096 rows: k = 14336 7.13 us
+// in quarters against 7.60 us in halves, k = 12288 6.49 against 7.20 us, k = 8192 5.06
+// against 4.97 us.  fp16 scales, no gated pairs, no fused rms_norm.  1: whole rows.
+static int k_parts(const QArgs& a) {
     static const bool off = [] {  // LUX_HIP_GEMV_NO_KSPLIT=1: whole rows per wave (A/B timing)
         const char* e = getenv("LUX_HIP_GEMV_NO_KSPLIT");
         return e && e[0] == '1';
     }();
     const int target_waves = device_cus() * 8;
-    return !off && a.scale_kind == ScaleKind::F16 && a.epi.kind != (int)Epi::SiluMul && !a.rn.gamma &&
-           a.n_out <= 2 * target_waves && a.k >= 4096 && a.k % 64 == 0 && a.k / 2 <= 8192;
+    if (off || a.scale_kind != ScaleKind::F16 || a.epi.kind == (int)Epi::SiluMul || a.rn.gamma ||
+        a.n_out > 2 * target_waves || a.k < 4096 || a.k % 64 != 0 || a.k > 16384)
+        return 1;
+    return a.k > 8192 && a.k % 128 == 0 ? 4 : 2;
 }
 
 // RN (the GEMV normalises its own row): one to four slices per lane (k <= 8192), so that
@@ -326,7 +335,12 @@ template <ScaleKind SK, YKind YK, bool RN>
 static bool dispatch_spl(const QArgs& a, hipStream_t s) {
     const int slices = a.k / 32;
     if constexpr (SK == ScaleKind::F16 && !RN) {
-        if (use_k_halves(a)) {
+        const int kp = k_parts(a);
+        if (kp == 4) {  // 8192 < k <= 16384: 65 to 128 slices per quarter
+            launch_fast<2, SK, YK, RN, 4>(a, s);
+            return true;
+        }
+        if (kp == 2) {
             const int sph = (slices / 2 + 63) / 64;  // slices per lane in each half
             if (sph <= 1) launch_fast<1, SK, YK, RN, 2>(a, s);
             else if (sph <= 2) launch_fast<2, SK, YK, RN, 2>(a, s);
@@ -390,14 +404,14 @@ bool qgemv_i4_fast(const QArgs& a) {
 }
 
 // The fused form stays bit-identical to rms_norm followed by the plain GEMV only where the
-// plain GEMV gives whole rows to one wave; shapes it splits into k halves run both kernels.
+// plain GEMV gives whole rows to one wave; shapes whose k it splits run both kernels.
 bool qgemv_i4_rn_supported(const QArgs& a) {
     QArgs plain = a;
     plain.rn.gamma = nullptr;
     QArgs b = a;
     if (!b.rn.gamma) b.rn.gamma = reinterpret_cast<const float*>(16);  // only the x-alignment test differs
     return a.m == 1 && a.wbits == 4 && a.scale_kind == ScaleKind::F16 && a.k <= 8192 && qgemv_i4_fast(b) &&
-           !use_k_halves(plain);
+           k_parts(plain) == 1;
 }
 
 hipError_t launch_qgemv_i4(const QArgs& a, hipStream_t s) {

@@ -80,6 +80,22 @@ def test_gemv_f32_rows_split_between_waves(ctx, M, N, lda):
     compare(ctx.download(yb, np.float32, M), ref, f"gemv split {M}x{N}", rel_tol=1e-5)
 
 
+@pytest.mark.parametrize("M,K,lda", [(4096, 4096, 4096), (8192, 4096, 4100), (2048, 2048, 2048),
+                                     (3000, 2048, 2052), (1024, 1024, 1024), (1500, 4096, 4096)])
+def test_gemv_f32_rows_in_k_quarters(ctx, M, K, lda):
+    """Few rows with k in {1024, 2048, 4096}: four waves per row set, one per quarter of k,
+    each wave 4, 8 or 16 rows; ragged last row sets (1500, 3000) compute clamped rows and
+    store only their own."""
+    r = rng(M * 3 + K)
+    A = r.standard_normal((M, lda)).astype(np.float32)
+    x = r.standard_normal(K).astype(np.float32)
+    y0 = r.standard_normal(M).astype(np.float32)
+    ref = oracle.gemv_row_parallel(A, x, y0, 1.25, 0.5, lda=lda, rows=M, cols=K)
+    a, xb, yb = ctx.upload(A), ctx.upload(x), ctx.upload(y0)
+    ctx.gemv_f32(a, xb, yb, M, K, 1.25, 0.5, lda=lda)
+    compare(ctx.download(yb, np.float32, M), ref, f"gemv quarters {M}x{K}", rel_tol=1e-5)
+
+
 @pytest.mark.parametrize("M,K,N", [(64, 64, 64), (100, 37, 70), (1, 512, 300), (257, 129, 3),
                                    (512, 1024, 256)])
 def test_matmul_f32_general(ctx, M, K, N):

@@ -104,6 +104,61 @@ __global__ __launch_bounds__(256) void k_gemv_f32(const float* __restrict__ A,
     }
 }
 
+// Few rows of fp32 (the config-1 shape, 4096 x 4096): each row splits into KS parts of
+// k and each wave owns RW rows of one part, CPL 16-byte chunks per lane and row, with the
+// next D rows' loads in flight while it computes a row.  The parts' sums meet in LDS and
+// are added in k order.  Needs K / 4 = 64 * KS * CPL chunks and the vector layout.
+// Measured at 4096 x 4096 (lab, same process): 16 rows per wave in 1,024 waves 11.14 us,
+// 8 rows in 2,048 waves 11.26 us, 32 rows 12.4 us; one or three rows ahead instead of two
+// within 0.2 %.
+template <int RW, int KS, int CPL, int D = 2>
+__global__ __launch_bounds__(256) void k_gemv_f32_parts(const float* __restrict__ A, const float* __restrict__ x,
+                                                        float* __restrict__ y, int M, int K, int lda, float alpha,
+                                                        float beta) {
+    constexpr int RS = 4 / KS;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int row0 = (blockIdx.x * RS + wave % RS) * RW, kp = wave / RS;
+    const int nrows = min(RW, M - row0);
+    const int c0 = kp * (64 * CPL) + lane;  // the lane's first chunk in the row
+    const f32x4* x4 = reinterpret_cast<const f32x4*>(x);
+    f32x4 xr[CPL];
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) xr[c] = x4[c0 + 64 * c];
+    f32x4 q[RW][CPL];
+    auto issue = [&](int r) {
+        const f32x4* a4 = reinterpret_cast<const f32x4*>(A + (size_t)min(row0 + r, M - 1) * lda);
+#pragma unroll
+        for (int c = 0; c < CPL; ++c) q[r][c] = __builtin_nontemporal_load(a4 + c0 + 64 * c);
+    };
+#pragma unroll
+    for (int r = 0; r < (D < RW ? D : RW); ++r) issue(r);
+    float res = 0.f;
+#pragma unroll
+    for (int r = 0; r < RW; ++r) {
+        if (r + D < RW) issue(r + D);
+        __builtin_amdgcn_sched_barrier(0);
+        float a0 = 0.f, a1 = 0.f;
+#pragma unroll
+        for (int c = 0; c < CPL; ++c) {
+            float& acc = (c & 1) ? a1 : a0;
+            acc = fmaf(q[r][c].x, xr[c].x, acc);
+            acc = fmaf(q[r][c].y, xr[c].y, acc);
+            acc = fmaf(q[r][c].z, xr[c].z, acc);
+            acc = fmaf(q[r][c].w, xr[c].w, acc);
+        }
+        const float d = wave_sum(a0 + a1);
+        res = lane == r ? d : res;
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    __shared__ float part_k[KS > 1 ? KS - 1 : 1][RS][64];
+    if (kp > 0) part_k[kp - 1][wave % RS][lane] = res;
+    __syncthreads();
+    float tot = res;
+#pragma unroll
+    for (int i = 0; i < KS - 1; ++i) tot += part_k[i][wave % RS][lane];
+    if (kp == 0 && lane < nrows) gemv_store(y + row0 + lane, tot, alpha, beta);
+}
+
 // Short rows (K <= 4L floats, L = 8, 16 or 32): a wave holds 64/L rows side by side,
 // L lanes each, and four such row groups per wave, so every lane keeps four 16-B loads
 // in flight as in the long-row kernel (a 128-float row would leave half of a one-row
@@ -498,6 +553,27 @@ hipError_t launch_gemv_f32_batched(const float* A, const float* x, float* y, int
     dim3 grid((unsigned)std::min<int64_t>(row_blocks, 1 << 20), (unsigned)std::min(batch, 65535)),
         block(256);
     const bool vec = (lda % 4 == 0) && aligned16(A) && aligned16(x) && sa % 4 == 0 && sx % 4 == 0;
+    if (mode == 3 && vec && M >= 1024 && (K == 1024 || K == 2048 || K == 4096)) {
+        // k in quarters, RW rows per wave (4096 x 4096: 11.14 us against 11.58 us with
+        // the rows split in halves, one half row per wave)
+        const int rw = M >= 4096 ? 16 : M >= 2048 ? 8 : 4;
+        const dim3 g((unsigned)((M + rw - 1) / rw)), b(256);  // four waves (quarters) per row set
+        auto gp = [&](auto kern) { hipLaunchKernelGGL(kern, g, b, 0, s, A, x, y, M, K, lda, alpha, beta); };
+        if (K == 4096) {
+            if (rw == 16) gp(k_gemv_f32_parts<16, 4, 4>);
+            else if (rw == 8) gp(k_gemv_f32_parts<8, 4, 4>);
+            else gp(k_gemv_f32_parts<4, 4, 4>);
+        } else if (K == 2048) {
+            if (rw == 16) gp(k_gemv_f32_parts<16, 4, 2>);
+            else if (rw == 8) gp(k_gemv_f32_parts<8, 4, 2>);
+            else gp(k_gemv_f32_parts<4, 4, 2>);
+        } else {
+            if (rw == 16) gp(k_gemv_f32_parts<16, 4, 1>);
+            else if (rw == 8) gp(k_gemv_f32_parts<8, 4, 1>);
+            else gp(k_gemv_f32_parts<4, 4, 1>);
+        }
+        return hipGetLastError();
+    }
     if (mode == 3) grid.x = (unsigned)((M + 1) / 2);
     auto go = [&](auto kern) {
         hipLaunchKernelGGL(kern, grid, block, 0, s, A, x, y, M, K, lda, alpha, beta, batch, sa, sx, sy);

@@ -131,6 +131,20 @@ def test_gemv_f16(ctx, M, K):
     compare(ctx.download(yb, np.float32, M), ref, f"gemv_f16 {M}x{K}", rel_tol=1e-5)
 
 
+@pytest.mark.parametrize("M,K,lda", [(14336, 4096, 4096), (3000, 2048, 2056), (1024, 512, 512),
+                                     (20000, 1024, 1024), (2049, 4096, 4104)])
+def test_gemv_f16_rows_per_wave(ctx, M, K, lda):
+    """Whole rows of 512-4096 halves, 1-8 rows per wave at 8 waves per CU: ragged last waves
+    (3000, 2049 rows) compute clamped rows and store only their own; padded lda."""
+    r = rng(M + 5 * K)
+    A = r.standard_normal((M, lda)).astype(np.float16)
+    x = r.standard_normal(K).astype(np.float16)
+    ref = oracle.gemv_f16_f32(np.ascontiguousarray(A[:, :K]).view(np.uint16), x.view(np.uint16))
+    a, xb, yb = ctx.upload(A), ctx.upload(x), ctx.alloc(M * 4)
+    ctx.gemv_f16(a, xb, yb, M, K, lda=lda)
+    compare(ctx.download(yb, np.float32, M), ref, f"gemv_f16 rows {M}x{K} lda {lda}", rel_tol=1e-5)
+
+
 # --------------------------------------------------------------------------- gemv_batched
 @pytest.mark.parametrize("B,M,N,lda,pad_a,pad_x,pad_y", [
     (32, 2048, 128, 128, 0, 0, 0),    # 32 heads x 2048 keys x head dim 128, vector path

@@ -529,6 +529,59 @@ __global__ __launch_bounds__(256) void k_gemv_f16(const f16* __restrict__ A,
     if ((threadIdx.x & 63) == 0) y[row] = s;
 }
 
+// fp16 GEMV in the shape of k_gemv_f32_parts: rows split into KS parts of k, a wave owns
+// RW rows of one part, CPL 16-byte chunks (8 halves) per lane and row, two rows ahead;
+// exact fp16 products (v_dot2_f32_f16) summed in fp32, the parts' sums added in k order.
+// Needs K / 8 = 64 * KS * CPL chunks and the vector layout.  The launcher uses whole rows
+// (KS = 1) at 8 waves per CU: at 14336 x 4096, 7 rows per wave 18.34-18.38 us, quarters of
+// 14 rows in 4,096 waves 18.37-18.42 us, halves of 14 rows 18.7-18.8 us (lab).
+template <int RW, int KS, int CPL>
+__global__ __launch_bounds__(256) void k_gemv_f16_parts(const f16* __restrict__ A, const f16* __restrict__ x,
+                                                        float* __restrict__ y, int M, int lda) {
+    constexpr int RS = 4 / KS, D = 2;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int row0 = (blockIdx.x * RS + wave % RS) * RW, kp = wave / RS;
+    const int nrows = min(RW, M - row0);
+    const int c0 = kp * (64 * CPL) + lane;
+    const f16x8* x8 = reinterpret_cast<const f16x8*>(x);
+    f16x8 xr[CPL];
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) xr[c] = x8[c0 + 64 * c];
+    f16x8 q[RW][CPL];
+    auto issue = [&](int r) {
+        const f16x8* a8 = reinterpret_cast<const f16x8*>(A + (size_t)min(row0 + r, M - 1) * lda);
+#pragma unroll
+        for (int c = 0; c < CPL; ++c) q[r][c] = __builtin_nontemporal_load(a8 + c0 + 64 * c);
+    };
+#pragma unroll
+    for (int r = 0; r < (D < RW ? D : RW); ++r) issue(r);
+    float res = 0.f;
+#pragma unroll
+    for (int r = 0; r < RW; ++r) {
+        if (r + D < RW) issue(r + D);
+        __builtin_amdgcn_sched_barrier(0);
+        float a0 = 0.f, a1 = 0.f;
+#pragma unroll
+        for (int c = 0; c < CPL; ++c) {
+            const f16x8 v = q[r][c], u = xr[c];
+            a0 = __builtin_amdgcn_fdot2(f16x2{v[0], v[1]}, f16x2{u[0], u[1]}, a0, false);
+            a1 = __builtin_amdgcn_fdot2(f16x2{v[2], v[3]}, f16x2{u[2], u[3]}, a1, false);
+            a0 = __builtin_amdgcn_fdot2(f16x2{v[4], v[5]}, f16x2{u[4], u[5]}, a0, false);
+            a1 = __builtin_amdgcn_fdot2(f16x2{v[6], v[7]}, f16x2{u[6], u[7]}, a1, false);
+        }
+        const float d = wave_sum(a0 + a1);
+        res = lane == r ? d : res;
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    __shared__ float part_k[KS > 1 ? KS - 1 : 1][RS][64];
+    if (kp > 0) part_k[kp - 1][wave % RS][lane] = res;
+    if constexpr (KS > 1) __syncthreads();
+    float tot = res;
+#pragma unroll
+    for (int i = 0; i < KS - 1; ++i) tot += part_k[i][wave % RS][lane];
+    if (kp == 0 && lane < nrows) y[row0 + lane] = tot;
+}
+
 // dot_product_fp16_fp32 (fp_quantized.wgsl:418-469): vector v of a and of b starts at
 // element 2 * (v * stride / 2) (the WGSL reads whole f16 pairs from word base / 2, so an
 // odd base starts one element early) and has `size` elements.  One wave per vector.
@@ -653,12 +706,41 @@ hipError_t launch_dot_f16(const void* a, const void* b, float* out, int size, in
     return hipGetLastError();
 }
 
+template <int CPL>
+static void launch_gemv_f16_rows(const f16* a, const f16* xv, float* y, int M, int lda, hipStream_t s) {
+    const int target_waves = device_cus() * 8;
+    int rw = (M + target_waves - 1) / target_waves;
+    rw = rw < 1 ? 1 : rw > 8 ? 8 : rw;
+    auto go = [&](auto kern, int r) {
+        hipLaunchKernelGGL(kern, dim3((unsigned)(((M + r - 1) / r + 3) / 4)), dim3(256), 0, s, a, xv, y, M, lda);
+    };
+    switch (rw) {
+        case 1: go(k_gemv_f16_parts<1, 1, CPL>, 1); break;
+        case 2: go(k_gemv_f16_parts<2, 1, CPL>, 2); break;
+        case 3: go(k_gemv_f16_parts<3, 1, CPL>, 3); break;
+        case 4: go(k_gemv_f16_parts<4, 1, CPL>, 4); break;
+        case 5: go(k_gemv_f16_parts<5, 1, CPL>, 5); break;
+        case 6: go(k_gemv_f16_parts<6, 1, CPL>, 6); break;
+        case 7: go(k_gemv_f16_parts<7, 1, CPL>, 7); break;
+        default: go(k_gemv_f16_parts<8, 1, CPL>, 8); break;
+    }
+}
+
 hipError_t launch_gemv_f16(const void* A, const void* x, float* y, int M, int K, int lda,
                            hipStream_t s) {
     dim3 grid((M + 3) / 4), block(256);
     bool vec = (lda % 8 == 0) && aligned16(A) && aligned16(x);
     const f16* a = reinterpret_cast<const f16*>(A);
     const f16* xv = reinterpret_cast<const f16*>(x);
+    // Whole rows of 512 to 4096 halves: RW rows per wave, 8 waves per CU (14336 x 4096:
+    // 7 rows per wave, 18.34-18.38 us against 19.15 us for one row per wave, lab)
+    if (vec && M >= 1024 && (K == 512 || K == 1024 || K == 2048 || K == 4096)) {
+        if (K == 4096) launch_gemv_f16_rows<8>(a, xv, y, M, lda, s);
+        else if (K == 2048) launch_gemv_f16_rows<4>(a, xv, y, M, lda, s);
+        else if (K == 1024) launch_gemv_f16_rows<2>(a, xv, y, M, lda, s);
+        else launch_gemv_f16_rows<1>(a, xv, y, M, lda, s);
+        return hipGetLastError();
+    }
     if (vec) hipLaunchKernelGGL(k_gemv_f16<true>, grid, block, 0, s, a, xv, y, M, K, lda);
     else hipLaunchKernelGGL(k_gemv_f16<false>, grid, block, 0, s, a, xv, y, M, K, lda);
     return hipGetLastError();
